@@ -1,0 +1,254 @@
+// C ABI of libhydraserve_amd.so (declared in include/hydraserve_amd.h).
+//
+// Host-side validation mirrors the checks the reference performs in Python
+// before its Triton launches (hydraserve/kernels/awq.py:28-43,
+// hydraserve/kernels/fp8.py:28-62) and returns an error code instead of
+// launching on malformed input.  The launch plan (regime, tile shape, stream-K
+// grid, workspace size) is a pure function of (kind, M, N, K, CU count), so
+// hs_gemm_workspace_bytes and the GEMM entry points always agree.
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+
+#include "qgemm_common.h"
+#include "../../include/hydraserve_amd.h"
+
+namespace hsq {
+hipError_t launch_decode(int wt, const GemmArgs& a, int MT, int S, hipStream_t stream);
+hipError_t launch_prefill(int wt, const GemmArgs& a, int BM, hipStream_t stream);
+int decode_slot_floats(int MT, int S);
+int prefill_slot_floats(int BM);
+hipError_t launch_int4_dequant(const uint32_t* packed, int64_t ldw, const void* scale, int64_t lds, int sdt,
+                               const int32_t* zero, int64_t ldz, void* out, int64_t ldo, int odt, int N, int K,
+                               int group, hipStream_t stream);
+hipError_t launch_fp8_dequant(const uint8_t* w, int64_t ldw, const void* scale, int64_t lds, int sdt, void* out,
+                              int64_t ldo, int odt, int N, int K, hipStream_t stream);
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+constexpr int kDecodeMaxM = 64;
+// Arrival counters live at a fixed offset and size in every workspace, so the
+// region never overlaps the (dirty) partial tiles of a call with another shape.
+constexpr int64_t kMaxTiles = 1 << 18;
+constexpr int64_t kCounterBytes = kMaxTiles * 4;
+
+struct Tuning {
+  int decode_s = 0;        // strips of 16 rows per wave (0 = heuristic)
+  int decode_wg_per_cu = 0;
+  int prefill_bm = 0;
+  int prefill_wg_per_cu = 0;
+};
+
+int env_int(const char* name) {
+  const char* v = std::getenv(name);
+  return v ? std::atoi(v) : 0;
+}
+
+// Optional overrides for tuning sweeps, read once per process.
+const Tuning& tuning() {
+  static Tuning t = [] {
+    Tuning r;
+    r.decode_s = env_int("HS_DECODE_S");
+    r.decode_wg_per_cu = env_int("HS_DECODE_WG_PER_CU");
+    r.prefill_bm = env_int("HS_PREFILL_BM");
+    r.prefill_wg_per_cu = env_int("HS_PREFILL_WG_PER_CU");
+    return r;
+  }();
+  return t;
+}
+
+int device_cus() {
+  static int cus[kMaxDevices] = {0};
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+struct Plan {
+  bool decode = true;
+  int MT = 1, S = 1, BM = 256;
+  int T = 0, TM = 1, G = 0;
+  int64_t U = 0;
+  int P = 0;
+  int64_t slot_floats = 0;
+  int64_t counter_bytes = 0;
+  int64_t ws_bytes = 0;
+};
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+Plan make_plan(int M, int N, int K) {
+  Plan p;
+  const int cus = device_cus();
+  const Tuning& tn = tuning();
+  if (M <= kDecodeMaxM) {
+    p.decode = true;
+    p.MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+    int S = tn.decode_s;
+    if (S != 1 && S != 2 && S != 4) S = 1;
+    p.S = S;
+    p.T = static_cast<int>(cdiv(N, 64 * S));
+    p.TM = 1;
+    p.G = static_cast<int>(cdiv(K, 128));
+    const int occ = tn.decode_wg_per_cu > 0 ? tn.decode_wg_per_cu : 4;
+    p.U = static_cast<int64_t>(p.T) * p.G;
+    p.P = static_cast<int>(p.U < static_cast<int64_t>(cus) * occ ? p.U : static_cast<int64_t>(cus) * occ);
+    p.slot_floats = decode_slot_floats(p.MT, p.S);
+  } else {
+    p.decode = false;
+    int bm = tn.prefill_bm;
+    if (bm != 128 && bm != 256) bm = 128;
+    p.BM = bm;
+    p.TM = static_cast<int>(cdiv(M, bm));
+    p.T = p.TM * static_cast<int>(cdiv(N, 256));
+    p.G = static_cast<int>(cdiv(K, 64));
+    const int occ = tn.prefill_wg_per_cu > 0 ? tn.prefill_wg_per_cu : 1;
+    p.U = static_cast<int64_t>(p.T) * p.G;
+    p.P = static_cast<int>(p.U < static_cast<int64_t>(cus) * occ ? p.U : static_cast<int64_t>(cus) * occ);
+    p.slot_floats = prefill_slot_floats(bm);
+  }
+  p.counter_bytes = kCounterBytes;
+  p.ws_bytes = p.counter_bytes + static_cast<int64_t>(p.P) * 2 * p.slot_floats * 4;
+  return p;
+}
+
+int hip_code(hipError_t e) { return e == hipSuccess ? HS_OK : HS_EHIP + static_cast<int>(e); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool valid_dt(int dt) { return dt == HS_DT_BF16 || dt == HS_DT_F16 || dt == HS_DT_F32; }
+
+int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  const Plan p = make_plan(a.M, a.N, a.K);
+  if (p.T > kMaxTiles) return HS_EUNSUPPORTED;
+  if (workspace == nullptr || workspace_bytes < p.ws_bytes) return HS_EWORKSPACE;
+  a.G = p.G;
+  a.T = p.T;
+  a.TM = p.TM;
+  a.U = p.U;
+  a.P = p.P;
+  a.counters = reinterpret_cast<int*>(workspace);
+  a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.counter_bytes);
+  a.xvec = aligned16(a.x) && (a.ldx % 8 == 0);
+  hipError_t e = p.decode ? launch_decode(wt, a, p.MT, p.S, stream) : launch_prefill(wt, a, p.BM, stream);
+  return hip_code(e);
+}
+
+}  // namespace
+}  // namespace hsq
+
+extern "C" {
+
+int hs_abi_version(void) { return 1; }
+
+const char* hs_error_string(int code) {
+  switch (code) {
+    case HS_OK: return "success";
+    case HS_EINVAL: return "invalid argument (shape, stride, pointer or dtype code)";
+    case HS_EWORKSPACE: return "workspace missing or smaller than hs_gemm_workspace_bytes()";
+    case HS_EUNSUPPORTED: return "unsupported configuration";
+    default: break;
+  }
+  if (code >= HS_EHIP) return hipGetErrorString(static_cast<hipError_t>(code - HS_EHIP));
+  return "unknown error";
+}
+
+int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
+  if ((kind != HS_KIND_INT4 && kind != HS_KIND_FP8) || M <= 0 || N <= 0 || K <= 0) return 0;
+  return hsq::make_plan(M, N, K).ws_bytes;
+}
+
+int hs_int4_gemm(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,
+                 int64_t ld_scale, int scale_dtype, const int32_t* zero_point, int64_t ld_zero, void* y, int64_t ldy,
+                 int M, int N, int K, int group, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return HS_EINVAL;
+  if (group != 128) return HS_EUNSUPPORTED;
+  if (M == 0 || N == 0) return HS_OK;
+  if (K == 0) return HS_EUNSUPPORTED;
+  const int64_t kw = (K + 7) / 8, groups = (K + 127) / 128;
+  if (!x || !packed || !scale || !zero_point || !y) return HS_EINVAL;
+  if (ldx < K || ld_packed < kw || ld_scale < groups || ld_zero < groups || ldy < N) return HS_EINVAL;
+  if (!hsq::valid_dt(scale_dtype)) return HS_EINVAL;
+  hsq::GemmArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.w = packed;
+  a.ldw = ld_packed;
+  a.scale = scale;
+  a.lds = ld_scale;
+  a.sdt = scale_dtype;
+  a.zero = zero_point;
+  a.ldz = ld_zero;
+  a.y = static_cast<uint16_t*>(y);
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.wvec = hsq::aligned16(packed) && (ld_packed % 4 == 0);
+  return hsq::run_gemm(hsq::W_INT4, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int hs_fp8_gemm(const void* x, int64_t ldx, const uint8_t* data, int64_t ld_data, const void* scale_inv,
+                int64_t ld_scale, int scale_dtype, void* y, int64_t ldy, int M, int N, int K, void* workspace,
+                int64_t workspace_bytes, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return HS_EINVAL;
+  if (M == 0 || N == 0) return HS_OK;
+  if (K == 0) return HS_EUNSUPPORTED;
+  const int64_t kb = (K + 127) / 128;
+  if (!x || !data || !scale_inv || !y) return HS_EINVAL;
+  if (ldx < K || ld_data < K || ld_scale < kb || ldy < N) return HS_EINVAL;
+  if (!hsq::valid_dt(scale_dtype)) return HS_EINVAL;
+  hsq::GemmArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.w = data;
+  a.ldw = ld_data;
+  a.scale = scale_inv;
+  a.lds = ld_scale;
+  a.sdt = scale_dtype;
+  a.zero = nullptr;
+  a.ldz = 0;
+  a.y = static_cast<uint16_t*>(y);
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.wvec = hsq::aligned16(data) && (ld_data % 16 == 0);
+  return hsq::run_gemm(hsq::W_FP8, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int hs_int4_dequant(const int32_t* packed, int64_t ld_packed, const void* scale, int64_t ld_scale, int scale_dtype,
+                    const int32_t* zero_point, int64_t ld_zero, void* out, int64_t ld_out, int out_dtype, int N, int K,
+                    int group, void* stream) {
+  if (N < 0 || K < 0 || group <= 0) return HS_EINVAL;
+  if (N == 0 || K == 0) return HS_OK;
+  const int64_t kw = (K + 7) / 8, groups = (K + group - 1) / group;
+  if (!packed || !scale || !zero_point || !out) return HS_EINVAL;
+  if (ld_packed < kw || ld_scale < groups || ld_zero < groups || ld_out < K) return HS_EINVAL;
+  if (!hsq::valid_dt(scale_dtype) || !hsq::valid_dt(out_dtype)) return HS_EINVAL;
+  return hsq::hip_code(hsq::launch_int4_dequant(reinterpret_cast<const uint32_t*>(packed), ld_packed, scale, ld_scale,
+                                                scale_dtype, zero_point, ld_zero, out, ld_out, out_dtype, N, K, group,
+                                                static_cast<hipStream_t>(stream)));
+}
+
+int hs_fp8_dequant(const uint8_t* data, int64_t ld_data, const void* scale_inv, int64_t ld_scale, int scale_dtype,
+                   void* out, int64_t ld_out, int out_dtype, int N, int K, void* stream) {
+  if (N < 0 || K < 0) return HS_EINVAL;
+  if (N == 0 || K == 0) return HS_OK;
+  const int64_t kb = (K + 127) / 128;
+  if (!data || !scale_inv || !out) return HS_EINVAL;
+  if (ld_data < K || ld_scale < kb || ld_out < K) return HS_EINVAL;
+  if (!hsq::valid_dt(scale_dtype) || !hsq::valid_dt(out_dtype)) return HS_EINVAL;
+  return hsq::hip_code(hsq::launch_fp8_dequant(data, ld_data, scale_inv, ld_scale, scale_dtype, out, ld_out, out_dtype,
+                                               N, K, static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

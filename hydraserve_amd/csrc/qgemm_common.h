@@ -1,0 +1,157 @@
+// Shared device helpers for the quantized weight-only GEMMs (gfx950 / CDNA4).
+//
+// Both weight formats compute Y[M,N] = X[M,K] . W[N,K]^T with bf16 X and Y and
+// fp32 accumulation, like hydraserve/kernels/awq.py:82-142 and
+// hydraserve/kernels/fp8.py:104-168, but the work decomposition is our own:
+//
+//   * a "unit" is (output tile, K chunk); units are numbered tile-major, so a
+//     contiguous range of units walks K inside one tile before moving on;
+//   * a persistent grid of P workgroups takes equal contiguous unit ranges
+//     (stream-K).  A workgroup whose range covers a whole tile stores bf16
+//     directly.  Tiles cut by a range boundary are finished by the last
+//     contributor to arrive: every contributor writes an fp32 partial into its
+//     own slot, bumps the tile's counter, and the last one sums the slots in
+//     workgroup order (deterministic) and stores bf16.  The last one also
+//     resets the counter, so the workspace stays zeroed between calls.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace hsq {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+enum WeightKind { W_INT4 = 0, W_FP8 = 1 };
+enum ScaleDtype { SCALE_BF16 = 0, SCALE_F16 = 1, SCALE_F32 = 2 };
+
+struct GemmArgs {
+  const uint16_t* x;  // bf16 activations [M, K], row stride ldx (elements)
+  int64_t ldx;
+  const void* w;      // INT4: int32 words [N, ceil(K/8)]; FP8: bytes [N, K]
+  int64_t ldw;        // row stride in words (INT4) or bytes (FP8)
+  const void* scale;  // INT4: [N, G128]; FP8: [ceil(N/128), ceil(K/128)]
+  int64_t lds;        // row stride of scale (elements)
+  int sdt;            // ScaleDtype
+  const int32_t* zero;  // INT4 zero points [ceil(N/8), G128], row stride ldz
+  int64_t ldz;
+  uint16_t* y;        // bf16 output [M, N], row stride ldy
+  int64_t ldy;
+  int M, N, K;
+  int G;              // K chunks per tile
+  int T;              // output tiles
+  int TM;             // tiles along M (prefill only; decode uses 1)
+  int64_t U;          // units = T * G
+  int P;              // persistent workgroups (P <= U)
+  int* counters;      // [T] arrival counters, zero between calls
+  float* partials;    // [P][2][slot] fp32 partial tiles
+  int xvec;           // X base and row stride allow 16-byte loads
+  int wvec;           // W base and row stride allow 16-byte loads
+};
+
+template <int SDT>
+__device__ __forceinline__ float load_scale(const void* p, int64_t idx) {
+  if constexpr (SDT == SCALE_F32) {
+    return reinterpret_cast<const float*>(p)[idx];
+  } else {
+    const uint32_t h = reinterpret_cast<const uint16_t*>(p)[idx];
+    if constexpr (SDT == SCALE_BF16) return __uint_as_float(h << 16);
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(h)));
+  }
+}
+
+__device__ __forceinline__ float load_scale_rt(const void* p, int64_t idx, int dt) {
+  if (dt == SCALE_F32) return load_scale<SCALE_F32>(p, idx);
+  if (dt == SCALE_BF16) return load_scale<SCALE_BF16>(p, idx);
+  return load_scale<SCALE_F16>(p, idx);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Two floats -> packed bf16x2, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ uint16_t to_bf16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// x & m, hidden from the optimizer so that byte extraction of the result
+// stays v_cvt_f32_ubyte{0..3} (one op per nibble) instead of being folded into
+// v_bfe_u32 + convert (two ops per nibble).
+__device__ __forceinline__ uint32_t opaque_and(uint32_t x, uint32_t m) {
+  uint32_t r;
+  asm volatile("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(m));
+  return r;
+}
+
+// ---- stream-K bookkeeping -------------------------------------------------
+__device__ __forceinline__ int64_t unit_begin(int p, int64_t U, int P) {
+  return (static_cast<int64_t>(p) * U) / P;
+}
+
+// Workgroup whose unit range holds unit u.
+__device__ __forceinline__ int unit_owner(int64_t u, int64_t U, int P) {
+  int p = static_cast<int>((u * P) / U);
+  if (p > P - 1) p = P - 1;
+  while (p + 1 < P && unit_begin(p + 1, U, P) <= u) ++p;
+  while (p > 0 && unit_begin(p, U, P) > u) --p;
+  return p;
+}
+
+// Slot of workgroup p's partial for tile t: 0 if t is p's first tile, else 1.
+__device__ __forceinline__ int partial_slot(int p, int t, int G, int64_t U, int P) {
+  return (unit_begin(p, U, P) / G == t) ? 0 : 1;
+}
+
+// Partial tiles cross workgroups that may run on different XCDs, whose L2s are
+// not coherent with each other.  Instead of agent-scope release/acquire
+// fences (which write back and invalidate the whole L2), partials are written
+// with write-through agent-scope stores and read with agent-scope loads, and
+// the arrival counter is an agent-scope atomic.
+__device__ __forceinline__ void store_partial(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_partial(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Count this workgroup's arrival at tile t once every thread's partial stores
+// are acknowledged; true in every thread of the workgroup that arrived last.
+__device__ __forceinline__ bool arrive_last(int* counters, int t, int contributors, int* lds_flag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(&counters[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *lds_flag = (old == contributors - 1);
+  }
+  __syncthreads();
+  return *lds_flag != 0;
+}
+
+__device__ __forceinline__ void reset_counter(int* counters, int t) {
+  if (threadIdx.x == 0) __hip_atomic_store(&counters[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// (tile, chunk) position of a unit, advanced without divisions.
+struct Cursor {
+  int t, c;
+  __device__ __forceinline__ void advance(int G) {
+    if (++c == G) {
+      c = 0;
+      ++t;
+    }
+  }
+};
+
+}  // namespace hsq

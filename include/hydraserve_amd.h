@@ -1,0 +1,106 @@
+/* hydraserve_amd: MI355X (gfx950) quantized weight-only linear layers.
+ *
+ * C ABI of libhydraserve_amd.so.  Plain pointers and sizes only; every device
+ * pointer is caller-owned memory on the current HIP device, every call is
+ * enqueued on `stream` with no host synchronisation and no allocation, so the
+ * calls are safe under HIP graph capture.
+ *
+ * Return value: 0 on success, otherwise an HS_E* code (see hs_error_string).
+ *
+ * Data layouts (exactly the reference's tensors, no repacking):
+ *   INT4 ("compressed-tensors" asymmetric, group 128):
+ *     packed     int32 [N, ceil(K/8)]   nibble i of word j = W[n, 8j+i]
+ *     scale      bf16/f16/f32 [N, ceil(K/128)]
+ *     zero_point int32 [ceil(N/8), ceil(K/128)]  nibble j of word [r,g] = zp[8r+j, g]
+ *   FP8 (E4M3FN, 128x128 blocks):
+ *     data       uint8 [N, K]
+ *     scale_inv  bf16/f16/f32 [ceil(N/128), ceil(K/128)]
+ *   Activations X: bf16 [M, K]; output Y: bf16 [M, N]; strides in elements
+ *   (INT4 packed: int32 words; FP8 data: bytes).
+ */
+#ifndef HYDRASERVE_AMD_H
+#define HYDRASERVE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* error codes */
+#define HS_OK 0
+#define HS_EINVAL 1        /* bad shape, stride, pointer or enum */
+#define HS_EWORKSPACE 2    /* workspace missing or smaller than hs_gemm_workspace_bytes() */
+#define HS_EUNSUPPORTED 3  /* valid request this library does not implement (e.g. group != 128) */
+#define HS_EHIP 1000       /* HS_EHIP + hipError_t from a HIP runtime call */
+
+/* scale / output dtype codes */
+#define HS_DT_BF16 0
+#define HS_DT_F16 1
+#define HS_DT_F32 2
+
+/* weight kinds for hs_gemm_workspace_bytes */
+#define HS_KIND_INT4 0
+#define HS_KIND_FP8 1
+
+/* ABI version of this header (bumped on any signature change). */
+int hs_abi_version(void);
+
+/* Static text for an error code. */
+const char* hs_error_string(int code);
+
+/* Bytes of device workspace hs_int4_gemm / hs_fp8_gemm need for this problem
+ * on the current device (0 if none).  The workspace holds a fixed 1 MiB
+ * block of per-tile arrival counters followed by fp32 partial tiles of the K
+ * split.  Problems with more than 2^18 output tiles return HS_EUNSUPPORTED.  It must be zero-filled once
+ * when allocated; every call leaves it zero-filled again, so it can be reused
+ * by later calls on the same stream.  Calls that overlap in time (different
+ * streams) must use different workspaces. */
+int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K);
+
+/* Y[M,N] = X[M,K] . dequant(W)^T, fp32 accumulation, bf16 output.
+ * Replaces the GPU branch of awq_linear (hydraserve/kernels/awq.py:25-75,
+ * Triton kernel awq.py:82-142).  group must be 128 (awq.py:30-31). */
+int hs_int4_gemm(const void* x, int64_t ldx,
+                 const int32_t* packed, int64_t ld_packed,
+                 const void* scale, int64_t ld_scale, int scale_dtype,
+                 const int32_t* zero_point, int64_t ld_zero,
+                 void* y, int64_t ldy,
+                 int M, int N, int K, int group,
+                 void* workspace, int64_t workspace_bytes,
+                 void* stream);
+
+/* Y[M,N] = X[M,K] . (decode(W) * scale_inv[n/128, k/128])^T, fp32 accumulation,
+ * bf16 output.  Replaces the GPU branch of fp8_linear
+ * (hydraserve/kernels/fp8.py:24-97, Triton kernel fp8.py:104-168). */
+int hs_fp8_gemm(const void* x, int64_t ldx,
+                const uint8_t* data, int64_t ld_data,
+                const void* scale_inv, int64_t ld_scale, int scale_dtype,
+                void* y, int64_t ldy,
+                int M, int N, int K,
+                void* workspace, int64_t workspace_bytes,
+                void* stream);
+
+/* out[N,K] = (q - z) * s rounded once to out_dtype (the dtype of the scale in
+ * the reference).  GPU counterpart of dequantize_int4_weight
+ * (hydraserve/kernels/awq.py:6-22); bit-exact. */
+int hs_int4_dequant(const int32_t* packed, int64_t ld_packed,
+                    const void* scale, int64_t ld_scale, int scale_dtype,
+                    const int32_t* zero_point, int64_t ld_zero,
+                    void* out, int64_t ld_out, int out_dtype,
+                    int N, int K, int group, void* stream);
+
+/* out[N,K] = decode(W) * cast(scale_inv, out_dtype), rounded to out_dtype.
+ * GPU counterpart of dequantize_fp8_weight (hydraserve/kernels/fp8.py:6-21);
+ * bit-exact. */
+int hs_fp8_dequant(const uint8_t* data, int64_t ld_data,
+                   const void* scale_inv, int64_t ld_scale, int scale_dtype,
+                   void* out, int64_t ld_out, int out_dtype,
+                   int N, int K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HYDRASERVE_AMD_H */

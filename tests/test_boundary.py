@@ -1,0 +1,164 @@
+"""CPU tests of the drop-in boundary: the C ABI, validation, fusion helpers.
+
+No HIP kernel runs here.  Validation order and messages follow
+hydraserve/kernels/awq.py:28-43 and hydraserve/kernels/fp8.py:28-62.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import hydraserve_amd as hs
+from hydraserve_amd import _native
+from hydraserve_amd.model.weights import BlockScaledFP8Weight, PackedInt4Weight
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_symbols():
+    text = (ROOT / "include" / "hydraserve_amd.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(hs_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    syms = header_symbols()
+    assert len(syms) >= 7
+    handle = ctypes.CDLL(str(_native.LIB_PATH))
+    for name in syms:
+        assert hasattr(handle, name), name
+    assert set(syms) == set(_native.SIGNATURES)
+
+
+def test_abi_version_and_errors():
+    L = _native.lib()
+    assert L.hs_abi_version() == _native.ABI_VERSION
+    assert L.hs_error_string(0) == b"success"
+    assert b"workspace" in L.hs_error_string(2)
+
+
+def test_c_validation_rejects_bad_args_without_launching():
+    L = _native.lib()
+    # group != 128
+    assert L.hs_int4_gemm(1, 256, 1, 32, 1, 2, 0, 1, 2, 1, 64, 1, 64, 256, 64, 1, 1 << 20, None) == 3
+    # null pointers
+    assert L.hs_int4_gemm(None, 256, None, 32, None, 2, 0, None, 2, None, 64, 1, 64, 256, 128, None, 0, None) == 1
+    # stride too small
+    assert L.hs_fp8_gemm(1, 10, 1, 256, 1, 2, 0, 1, 64, 1, 64, 256, 1, 1 << 20, None) == 1
+    # bad scale dtype code
+    assert L.hs_fp8_gemm(1, 256, 1, 256, 1, 2, 7, 1, 64, 1, 64, 256, 1, 1 << 20, None) == 1
+    # missing workspace is reported before any launch
+    assert L.hs_fp8_gemm(16, 256, 16, 256, 16, 2, 0, 16, 64, 1, 64, 256, None, 0, None) == 2
+    # empty problems are no-ops
+    assert L.hs_int4_gemm(None, 0, None, 0, None, 0, 0, None, 0, None, 0, 0, 64, 256, 128, None, 0, None) == 0
+
+
+def test_workspace_size_is_deterministic_and_covers_counters():
+    L = _native.lib()
+    a = L.hs_gemm_workspace_bytes(0, 1, 34816, 5120)
+    assert a == L.hs_gemm_workspace_bytes(0, 1, 34816, 5120) and a > 0
+    assert L.hs_gemm_workspace_bytes(0, 0, 64, 64) == 0
+    assert L.hs_gemm_workspace_bytes(9, 1, 64, 64) == 0
+
+
+def _int4_weight(n=64, k=256, group=128):
+    g = (k + group - 1) // group
+    return PackedInt4Weight(
+        torch.zeros(n, k // 8, dtype=torch.int32),
+        torch.ones(n, g, dtype=torch.bfloat16),
+        torch.zeros(n // 8, g, dtype=torch.int32),
+        (n, k),
+        group,
+    )
+
+
+def _fp8_weight(n=129, k=129):
+    return BlockScaledFP8Weight(
+        torch.zeros(n, k, dtype=torch.float8_e4m3fn),
+        torch.ones((n + 127) // 128, (k + 127) // 128, dtype=torch.bfloat16),
+        (n, k),
+    )
+
+
+def test_awq_validation_order_and_messages():
+    w = _int4_weight()
+    with pytest.raises(ValueError, match="activation width does not match packed INT4 weight"):
+        hs.awq_linear(torch.zeros(2, 128, dtype=torch.bfloat16), w)
+    w64 = _int4_weight(group=64)
+    with pytest.raises(ValueError, match="requires group_size=128"):
+        hs.awq_linear(torch.zeros(2, 256, dtype=torch.bfloat16), w64)
+
+
+def test_awq_cpu_activation_is_an_error_not_a_fallback():
+    with pytest.raises(RuntimeError, match="ROCm GPU only"):
+        hs.awq_linear(torch.zeros(2, 256, dtype=torch.bfloat16), _int4_weight())
+
+
+def test_fp8_validation_order_and_messages():
+    w = _fp8_weight()
+    with pytest.raises(ValueError, match="activation width does not match FP8 weight"):
+        hs.fp8_linear(torch.zeros(1, 128), w)
+    bad_block = BlockScaledFP8Weight(w.data, w.scale_inv, w.original_shape, (64, 64))
+    with pytest.raises(ValueError, match="128x128 blocks"):
+        hs.fp8_linear(torch.zeros(1, 129), bad_block)
+    # the reference test tests/test_fp8_kernel.py:117-123
+    invalid = BlockScaledFP8Weight(w.data, w.scale_inv[:1, :1], w.original_shape)
+    with pytest.raises(ValueError, match="scale grid"):
+        hs.fp8_linear(torch.randn(1, 129), invalid)
+    with pytest.raises(RuntimeError, match="ROCm GPU only"):
+        hs.fp8_linear(torch.zeros(1, 129, dtype=torch.bfloat16), w)
+
+
+def test_dequantize_validates_scale_grid_first():
+    w = _fp8_weight()
+    invalid = BlockScaledFP8Weight(w.data, w.scale_inv[:1, :1], w.original_shape)
+    with pytest.raises(ValueError, match="scale grid"):
+        hs.dequantize_fp8_weight(invalid)
+
+
+def test_concat_split_round_trip_int4_and_fp8():
+    # tests/test_runtime.py:394-431 in the reference: concat then split returns the parts.
+    g = torch.Generator().manual_seed(0)
+    parts = []
+    for n in (16, 8, 24):
+        parts.append(
+            PackedInt4Weight(
+                torch.randint(-(2**31), 2**31 - 1, (n, 32), generator=g, dtype=torch.int32),
+                torch.rand(n, 2, generator=g).to(torch.bfloat16),
+                torch.randint(-(2**31), 2**31 - 1, (n // 8, 2), generator=g, dtype=torch.int32),
+                (n, 256),
+            )
+        )
+    fused = hs.concatenate_linear_weights(parts)
+    assert fused.original_shape == (48, 256)
+    for a, b in zip(parts, hs.split_linear_weight(fused, (16, 8, 24))):
+        assert b.original_shape == a.original_shape
+        assert torch.equal(a.packed, b.packed) and torch.equal(a.scale, b.scale)
+        assert torch.equal(a.zero_point, b.zero_point)
+    # N % 8 != 0 cannot be fused (zero points pack 8 rows per word)
+    odd = PackedInt4Weight(parts[0].packed[:12], parts[0].scale[:12], parts[0].zero_point[:2], (12, 256))
+    assert hs.concatenate_linear_weights([odd, parts[1]]) is None
+
+    f_parts = [
+        BlockScaledFP8Weight(
+            torch.randint(0, 120, (n, 200), generator=g, dtype=torch.uint8).view(torch.float8_e4m3fn),
+            torch.rand(n // 128, 2, generator=g).to(torch.bfloat16),
+            (n, 200),
+        )
+        for n in (128, 256)
+    ]
+    fused = hs.concatenate_linear_weights(f_parts)
+    assert fused.original_shape == (384, 200) and fused.scale_inv.shape == (3, 2)
+    for a, b in zip(f_parts, hs.split_linear_weight(fused, (128, 256))):
+        assert torch.equal(a.data.view(torch.uint8), b.data.view(torch.uint8))
+        assert torch.equal(a.scale_inv, b.scale_inv)
+    bad = BlockScaledFP8Weight(f_parts[0].data[:100], f_parts[0].scale_inv, (100, 200))
+    assert hs.concatenate_linear_weights([bad, f_parts[1]]) is None
+
+
+def test_linear_dispatch_dense_branch():
+    w = torch.randn(5, 7)
+    x = torch.randn(3, 7)
+    torch.testing.assert_close(hs.linear(x, w), x @ w.T)
