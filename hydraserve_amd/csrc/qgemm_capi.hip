@@ -17,6 +17,10 @@ namespace hsq {
 hipError_t launch_decode(int wt, const GemmArgs& a, int MT, int S, hipStream_t stream);
 hipError_t launch_prefill(int wt, const GemmArgs& a, int BM, hipStream_t stream);
 int decode_slot_floats(int MT, int S);
+hipError_t launch_stream(int wt, const GemmArgs& a, int MT, int S, hipStream_t stream);
+int stream_slot_floats(int MT, int S);
+bool stream_ok(const GemmArgs& a, int wt, int NB);
+bool decode_kfull(int K, int xvec, int wvec);
 int prefill_slot_floats(int BM);
 hipError_t launch_int4_dequant(const uint32_t* packed, int64_t ldw, const void* scale, int64_t lds, int sdt,
                                const int32_t* zero, int64_t ldz, void* out, int64_t ldo, int odt, int N, int K,
@@ -34,6 +38,10 @@ constexpr int64_t kMaxTiles = 1 << 18;
 constexpr int64_t kCounterBytes = kMaxTiles * 4;
 
 struct Tuning {
+  int st_off = 0;          // 1: never use the streaming decode kernel
+  int st_s = 0;            // its strips of 16 rows per wave (0 = heuristic)
+  int st_wg = 0;           // its workgroups per CU
+  int st_nb = 0;           // its chunks per batch (0 = heuristic)
   int decode_s = 0;        // strips of 16 rows per wave (0 = heuristic)
   int decode_wg_per_cu = 0;
   int prefill_bm = 0;
@@ -49,6 +57,10 @@ int env_int(const char* name) {
 const Tuning& tuning() {
   static Tuning t = [] {
     Tuning r;
+    r.st_off = env_int("HS_ST_OFF");
+    r.st_s = env_int("HS_ST_S");
+    r.st_wg = env_int("HS_ST_WG");
+    r.st_nb = env_int("HS_ST_NB");
     r.decode_s = env_int("HS_DECODE_S");
     r.decode_wg_per_cu = env_int("HS_DECODE_WG_PER_CU");
     r.prefill_bm = env_int("HS_PREFILL_BM");
@@ -73,8 +85,9 @@ int device_cus() {
 }
 
 struct Plan {
+  bool stream = false;  // streaming decode kernel (fast path)
   bool decode = true;
-  int MT = 1, S = 1, BM = 256;
+  int MT = 1, S = 1, BM = 256, NB = 1;
   int T = 0, TM = 1, G = 0;
   int64_t U = 0;
   int P = 0;
@@ -85,11 +98,28 @@ struct Plan {
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-Plan make_plan(int M, int N, int K) {
+int stream_nb(int M) { return M <= 16 ? 8 : (M <= 32 ? 4 : 2); }
+
+// `fast`: the streaming kernel can run this problem (see stream_ok).
+Plan make_plan(int M, int N, int K, bool kfull, bool fast) {
   Plan p;
   const int cus = device_cus();
   const Tuning& tn = tuning();
-  if (M <= kDecodeMaxM) {
+  if (M <= kDecodeMaxM && fast && !tn.st_off) {
+    p.stream = true;
+    p.MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+    int S = tn.st_s;
+    if (S != 1 && S != 2) S = 1;
+    p.S = S;
+    p.NB = tn.st_nb > 0 ? tn.st_nb : stream_nb(M);
+    p.T = static_cast<int>(cdiv(N, 64 * S));
+    p.G = K / (128 * p.NB);
+    const int occ = tn.st_wg > 0 ? tn.st_wg : 1;
+    p.U = static_cast<int64_t>(p.T) * p.G;
+    const int64_t wgs = static_cast<int64_t>(cus) * occ;
+    p.P = static_cast<int>(p.U < wgs ? p.U : wgs);
+    p.slot_floats = stream_slot_floats(p.MT, S);
+  } else if (M <= kDecodeMaxM) {
     p.decode = true;
     p.MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     int S = tn.decode_s;
@@ -97,7 +127,8 @@ Plan make_plan(int M, int N, int K) {
     p.S = S;
     p.T = static_cast<int>(cdiv(N, 64 * S));
     p.TM = 1;
-    p.G = static_cast<int>(cdiv(K, 128));
+    p.NB = kfull ? 4 : 1;
+    p.G = static_cast<int>(cdiv(K, 128)) / p.NB;
     const int occ = tn.decode_wg_per_cu > 0 ? tn.decode_wg_per_cu : 4;
     p.U = static_cast<int64_t>(p.T) * p.G;
     p.P = static_cast<int>(p.U < static_cast<int64_t>(cus) * occ ? p.U : static_cast<int64_t>(cus) * occ);
@@ -127,18 +158,23 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 bool valid_dt(int dt) { return dt == HS_DT_BF16 || dt == HS_DT_F16 || dt == HS_DT_F32; }
 
 int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-  const Plan p = make_plan(a.M, a.N, a.K);
+  a.xvec = aligned16(a.x) && (a.ldx % 8 == 0);
+  const Tuning& tn = tuning();
+  const int nb = tn.st_nb > 0 ? tn.st_nb : stream_nb(a.M);
+  const Plan p = make_plan(a.M, a.N, a.K, decode_kfull(a.K, a.xvec, a.wvec), stream_ok(a, wt, nb));
   if (p.T > kMaxTiles) return HS_EUNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < p.ws_bytes) return HS_EWORKSPACE;
   a.G = p.G;
+  a.NB = p.NB;
   a.T = p.T;
   a.TM = p.TM;
   a.U = p.U;
   a.P = p.P;
   a.counters = reinterpret_cast<int*>(workspace);
   a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.counter_bytes);
-  a.xvec = aligned16(a.x) && (a.ldx % 8 == 0);
-  hipError_t e = p.decode ? launch_decode(wt, a, p.MT, p.S, stream) : launch_prefill(wt, a, p.BM, stream);
+  hipError_t e = p.stream   ? launch_stream(wt, a, p.MT, p.S, stream)
+                 : p.decode ? launch_decode(wt, a, p.MT, p.S, stream)
+                            : launch_prefill(wt, a, p.BM, stream);
   return hip_code(e);
 }
 
@@ -163,7 +199,14 @@ const char* hs_error_string(int code) {
 
 int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
   if ((kind != HS_KIND_INT4 && kind != HS_KIND_FP8) || M <= 0 || N <= 0 || K <= 0) return 0;
-  return hsq::make_plan(M, N, K).ws_bytes;
+  // The bound covers every variant the call may pick for this shape.
+  int64_t best = 0;
+  for (int kfull = 0; kfull < 2; ++kfull)
+    for (int fast = 0; fast < 2; ++fast) {
+      const int64_t b = hsq::make_plan(M, N, K, kfull != 0, fast != 0).ws_bytes;
+      best = b > best ? b : best;
+    }
+  return best;
 }
 
 int hs_int4_gemm(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,

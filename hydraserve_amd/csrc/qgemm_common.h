@@ -43,10 +43,11 @@ struct GemmArgs {
   uint16_t* y;        // bf16 output [M, N], row stride ldy
   int64_t ldy;
   int M, N, K;
-  int G;              // K chunks per tile
+  int G;              // stream-K steps per tile (decode: batches of NB chunks)
+  int NB;             // decode: K chunks per stream-K step
   int T;              // output tiles
   int TM;             // tiles along M (prefill only; decode uses 1)
-  int64_t U;          // units = T * G
+  int64_t U;          // stream-K steps = T * G
   int P;              // persistent workgroups (P <= U)
   int* counters;      // [T] arrival counters, zero between calls
   float* partials;    // [P][2][slot] fp32 partial tiles
@@ -56,6 +57,7 @@ struct GemmArgs {
 
 template <int SDT>
 __device__ __forceinline__ float load_scale(const void* p, int64_t idx) {
+  // idx is in elements of the scale dtype
   if constexpr (SDT == SCALE_F32) {
     return reinterpret_cast<const float*>(p)[idx];
   } else {

@@ -10,7 +10,7 @@
 // For every unit the workgroup stages the X chunk [M x 128] in LDS once and
 // each wavefront streams its weight strips straight from HBM into registers
 // with 16-byte loads (one INT4 strip-chunk = 16 rows x 64 B, one FP8
-// strip-chunk = 16 rows x 128 B), a few units ahead of use.
+// strip-chunk = 16 rows x 128 B), NBUF units ahead of use.
 //
 // Arithmetic.  Weights are decoded in registers and fed to
 // v_mfma_f32_16x16x32_bf16 with X padded to 16*MT rows.  The K order inside a
@@ -18,9 +18,9 @@
 // dot product unchanged), which lets every lane take one 16-byte run of a
 // weight row.
 //
-//   INT4: a nibble q is turned into the bf16 value 128+q by OR-ing it into the
-//   mantissa of 128.0 (0x4300), two nibbles per instruction.  For each group the
-//   MFMA yields T = sum_k x_k (128 + q_k); the true group sum is
+//   INT4: a nibble q is turned into the bf16 value 128+q by inserting it into
+//   the mantissa of 128.0 (0x4300), two nibbles per v_bfi_b32.  For each group
+//   the MFMA yields T = sum_k x_k (128 + q_k); the true group sum is
 //   sum_k x_k (q_k - z) = T - (128 + z) * Xg with Xg = sum_k x_k (computed once
 //   per chunk in LDS), then scaled by s and accumulated:
 //       acc += s * (T - (128 + z) * Xg).
@@ -32,12 +32,26 @@
 //   unit scale; every finite E4M3FN value, subnormals included, is a bf16).
 //   The 128x128 block scale is constant across a strip and a chunk, so it is
 //   applied once per chunk to the MFMA result: acc += s_block * T.
+//
+// KFULL variant: when K is a multiple of 128 and X / W rows are 16-byte
+// aligned, every load in the loop is an unconditional vector load (no branch,
+// so the compiler can keep NBUF units of loads in flight).  Other shapes use
+// the masked variant.
+#include <type_traits>
+
 #include "qgemm_common.h"
 
 namespace hsq {
 
 constexpr int DEC_THREADS = 256;
 constexpr int XS_STRIDE = 136;  // bf16 per LDS row: 128 + 8 pad (bank spread)
+
+// v_bfi_b32: (mask & src) | (~mask & base), one instruction.
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t src, uint32_t base) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(src), "v"(base));
+  return r;
+}
 
 template <int WT, int S>
 struct WRegs;
@@ -46,7 +60,7 @@ template <int S>
 struct WRegs<W_INT4, S> {
   u32x4_t q[S];
   float s[S];
-  float negc[S];  // -(128 + z)
+  uint32_t z[S];  // zero-point word (nibble selected at use)
 };
 
 template <int S>
@@ -55,10 +69,20 @@ struct WRegs<W_FP8, S> {
   float s[S];
 };
 
-template <int WT, int SDT, int MT, int S>
+// Per-strip row addresses for one tile (recomputed when the tile changes).
+template <int S>
+struct RowPtrs {
+  const uint8_t* w[S];   // weight row
+  const uint8_t* s[S];   // scale row (INT4: row n; FP8: row n/128)
+  const int32_t* z[S];   // INT4 zero-point row n/8
+  uint32_t zsh[S];       // INT4: 4 * (n % 8)
+};
+
+template <int WT, int SDT, int MT, int S, bool KFULL>
 struct Decode {
   static constexpr int NT = 64 * S;
   static constexpr int ROWS = 16 * MT;
+  static constexpr int SES = SDT == SCALE_F32 ? 4 : 2;  // scale element size
 
   struct Smem {
     __attribute__((aligned(16))) uint16_t xs[2][ROWS][XS_STRIDE];
@@ -66,34 +90,48 @@ struct Decode {
     int flag;
   };
 
-  // ---- weight loads ------------------------------------------------------
-  static __device__ __forceinline__ void load_w(const GemmArgs& a, WRegs<WT, S>& r, int t, int c,
-                                                int wave, int l16, int h) {
-    // `full` is uniform: the whole chunk is inside K and rows allow 16-byte loads.
-    const int kw = (a.K + 7) >> 3;  // INT4 words per row
-    const bool full = a.wvec && (WT == W_INT4 ? (c + 1) * 16 <= kw : (c + 1) * 128 <= a.K);
+  static __device__ __forceinline__ void set_rows(const GemmArgs& a, RowPtrs<S>& rp, int t, int wave, int l16) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       int row = t * NT + (wave * S + s) * 16 + l16;
       row = row < a.N ? row : a.N - 1;
       if constexpr (WT == W_INT4) {
-        const uint32_t* wp = reinterpret_cast<const uint32_t*>(a.w) + row * a.ldw;
+        rp.w[s] = reinterpret_cast<const uint8_t*>(a.w) + row * a.ldw * 4;
+        rp.s[s] = reinterpret_cast<const uint8_t*>(a.scale) + row * a.lds * SES;
+        rp.z[s] = a.zero + (row >> 3) * a.ldz;
+        rp.zsh[s] = (row & 7) * 4;
+      } else {
+        rp.w[s] = reinterpret_cast<const uint8_t*>(a.w) + row * a.ldw;
+        rp.s[s] = reinterpret_cast<const uint8_t*>(a.scale) + (row >> 7) * a.lds * SES;
+        rp.z[s] = nullptr;
+        rp.zsh[s] = 0;
+      }
+    }
+  }
+
+  // ---- weight loads ------------------------------------------------------
+  static __device__ __forceinline__ void load_w(const GemmArgs& a, WRegs<WT, S>& r, const RowPtrs<S>& rp, int c,
+                                                int h) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if constexpr (WT == W_INT4) {
+        const uint32_t* wp = reinterpret_cast<const uint32_t*>(rp.w[s]);
         const int w0 = c * 16 + 4 * h;
-        if (full) {
+        if constexpr (KFULL) {
           r.q[s] = *reinterpret_cast<const u32x4_t*>(wp + w0);
         } else {
+          const int kw = (a.K + 7) >> 3;
           u32x4_t v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = (w0 + e < kw) ? wp[w0 + e] : 0u;
           r.q[s] = v;
         }
-        r.s[s] = load_scale<SDT>(a.scale, row * a.lds + c);
-        const uint32_t zw = static_cast<uint32_t>(a.zero[(row >> 3) * a.ldz + c]);
-        r.negc[s] = -(128.0f + static_cast<float>((zw >> ((row & 7) * 4)) & 0xFu));
+        r.s[s] = load_scale<SDT>(rp.s[s], c);
+        r.z[s] = static_cast<uint32_t>(rp.z[s][c]);
       } else {
-        const uint8_t* wp = reinterpret_cast<const uint8_t*>(a.w) + row * a.ldw;
+        const uint8_t* wp = rp.w[s];
         const int b0 = c * 128 + 32 * h;
-        if (full) {
+        if constexpr (KFULL) {
           r.q[s][0] = *reinterpret_cast<const u32x4_t*>(wp + b0);
           r.q[s][1] = *reinterpret_cast<const u32x4_t*>(wp + b0 + 16);
         } else {
@@ -114,25 +152,26 @@ struct Decode {
             r.q[s][hh] = v;
           }
         }
-        r.s[s] = load_scale<SDT>(a.scale, (row >> 7) * a.lds + c);
+        r.s[s] = load_scale<SDT>(rp.s[s], c);
       }
     }
   }
 
   // ---- X staging -----------------------------------------------------------
   // Thread tid handles 16-byte segments idx = tid + 256*q: row idx/16, seg idx%16.
+  // KFULL: rows >= M load row M-1 (no branch); store_x never writes them.
   static __device__ __forceinline__ void load_x(const GemmArgs& a, u32x4_t (&xr)[MT], int c, int tid) {
-    const bool full = a.xvec && (c + 1) * 128 <= a.K;  // uniform
 #pragma unroll
     for (int q = 0; q < MT; ++q) {
       const int row = (tid >> 4) + 16 * q;
       const int k0 = c * 128 + (tid & 15) * 8;
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (row < a.M) {
-        const uint16_t* xp = a.x + row * a.ldx;
-        if (full) {
-          v = *reinterpret_cast<const u32x4_t*>(xp + k0);
-        } else {
+      if constexpr (KFULL) {
+        const int rc = row < a.M ? row : a.M - 1;
+        xr[q] = *reinterpret_cast<const u32x4_t*>(a.x + rc * a.ldx + k0);
+      } else {
+        u32x4_t v = {0u, 0u, 0u, 0u};
+        if (row < a.M) {
+          const uint16_t* xp = a.x + row * a.ldx;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const uint32_t lo = (k0 + 2 * e < a.K) ? xp[k0 + 2 * e] : 0u;
@@ -140,8 +179,8 @@ struct Decode {
             v[e] = lo | (hi << 16);
           }
         }
+        xr[q] = v;
       }
-      xr[q] = v;
     }
   }
 
@@ -150,15 +189,18 @@ struct Decode {
 #pragma unroll
     for (int q = 0; q < MT; ++q) {
       const int row = (tid >> 4) + 16 * q;
-      if (row >= a.M) continue;  // rows >= M stay zero (set once)
+      if (16 * q >= a.M) continue;  // uniform: a 16-row block wholly past M stays zero
       const int seg = tid & 15;
       u32x4_t v = xr[q];
+      const bool live = row < a.M;  // rows past M (clamped loads) must stay zero
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = live ? v[e] : 0u;
       if constexpr (WT == W_INT4) {
         // Per-row sum of the chunk (exact bf16 values, fp32 adds).
         float part = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          part += bf16_to_f32(v[e] & 0xFFFFu) + bf16_to_f32(v[e] >> 16);
+          part += __uint_as_float(v[e] << 16) + __uint_as_float(v[e] & 0xFFFF0000u);
         part += __shfl_xor(part, 1, 16);
         part += __shfl_xor(part, 2, 16);
         part += __shfl_xor(part, 4, 16);
@@ -178,7 +220,8 @@ struct Decode {
 
   // ---- one unit of MFMA work -----------------------------------------------
   static __device__ __forceinline__ void compute(const Smem& sm, int b, const WRegs<WT, S>& r,
-                                                 f32x4_t (&acc)[S][MT], int l16, int h) {
+                                                 const RowPtrs<S>& rp, f32x4_t (&acc)[S][MT], int l16, int h,
+                                                 uint32_t nib_mask, uint32_t magic) {
     bf16x8_t A[MT][4];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
@@ -199,10 +242,10 @@ struct Decode {
         for (int j = 0; j < 4; ++j) {
           const uint32_t w = r.q[s][j];
           u32x4_t p;
-          p[0] = (w & 0x000F000Fu) | 0x43004300u;
-          p[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-          p[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-          p[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+          p[0] = bfi(nib_mask, w, magic);
+          p[1] = bfi(nib_mask, w >> 4, magic);
+          p[2] = bfi(nib_mask, w >> 8, magic);
+          p[3] = bfi(nib_mask, w >> 12, magic);
           B[j] = __builtin_bit_cast(bf16x8_t, p);
         }
       } else {
@@ -218,6 +261,8 @@ struct Decode {
           B[j] = __builtin_bit_cast(bf16x8_t, p);
         }
       }
+      float negc = 0.f;
+      if constexpr (WT == W_INT4) negc = -(128.0f + static_cast<float>((r.z[s] >> rp.zsh[s]) & 0xFu));
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         f32x4_t tmp = {0.f, 0.f, 0.f, 0.f};
@@ -226,7 +271,7 @@ struct Decode {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           if constexpr (WT == W_INT4) {
-            acc[s][i][e] = fmaf(r.s[s], fmaf(r.negc[s], X[i][e], tmp[e]), acc[s][i][e]);
+            acc[s][i][e] = fmaf(r.s[s], fmaf(negc, X[i][e], tmp[e]), acc[s][i][e]);
           } else {
             acc[s][i][e] = fmaf(r.s[s], tmp[e], acc[s][i][e]);
           }
@@ -300,15 +345,25 @@ struct Decode {
   }
 };
 
-template <int WT, int SDT, int MT, int S, int NBUF>
+// Stream-K steps are batches of NB consecutive K chunks of one tile (the host
+// guarantees NB divides the chunk count), so every batch runs the same
+// unrolled, branch-free body: each of its NB units consumes one slot of the
+// register rings and refills that slot with the unit NB ahead.  Refills past
+// the workgroup's range reload its last unit (an L2 hit) instead of being
+// predicated, which keeps every load in the loop unconditional and counted.
+template <int WT, int SDT, int MT, int S, int NB, bool KFULL>
 __global__ __launch_bounds__(DEC_THREADS) void qgemm_decode_kernel(GemmArgs a) {
-  using D = Decode<WT, SDT, MT, S>;
+  using D = Decode<WT, SDT, MT, S, KFULL>;
   __shared__ typename D::Smem sm;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, l16 = lane & 15, h = lane >> 4;
   const int p = blockIdx.x;
-  const int64_t u0 = unit_begin(p, a.U, a.P), u1 = unit_begin(p + 1, a.U, a.P);
-  if (u0 >= u1) return;
+  const int64_t b0 = unit_begin(p, a.U, a.P), b1 = unit_begin(p + 1, a.U, a.P);
+  if (b0 >= b1) return;
+  const int GC = a.G * NB;  // chunks per tile
+  // Constants for the nibble -> bf16 insert, kept in VGPRs for v_bfi_b32.
+  const uint32_t nib_mask = opaque_and(0x000F000Fu, 0xFFFFFFFFu);
+  const uint32_t magic = opaque_and(0x43004300u, 0xFFFFFFFFu);
 
   // Rows M..16*MT-1 of both X buffers are zero for the whole kernel.
   for (int idx = tid; idx < 2 * D::ROWS * (XS_STRIDE / 2); idx += DEC_THREADS) {
@@ -320,70 +375,83 @@ __global__ __launch_bounds__(DEC_THREADS) void qgemm_decode_kernel(GemmArgs a) {
   for (int idx = tid; idx < 2 * D::ROWS; idx += DEC_THREADS)
     if ((idx % D::ROWS) >= a.M) sm.xsum[idx / D::ROWS][idx % D::ROWS] = 0.f;
 
-  const int n_units = static_cast<int>(u1 - u0);
-  Cursor cur{static_cast<int>(u0 / a.G), static_cast<int>(u0 % a.G)};
-  Cursor ld = cur;  // next unit whose weights are to be loaded
-  u32x4_t xr[MT];
-  D::load_x(a, xr, cur.c, tid);
-  WRegs<WT, S> wr[NBUF];
-#pragma unroll
-  for (int r = 0; r < NBUF; ++r)
-    if (r < n_units) {
-      D::load_w(a, wr[r], ld.t, ld.c, wave, l16, h);
-      ld.advance(a.G);
+  // Unit cursors (tile, chunk): `cur` is the unit being computed, `ld` the
+  // next unit to load.  `ld` stops at the last unit of the range.
+  const int first = static_cast<int>(b0) * NB, last = static_cast<int>(b1) * NB - 1;
+  Cursor cur{first / GC, first % GC};
+  Cursor ld = cur;
+  int ld_lin = first;
+  RowPtrs<S> lrp, rp;
+  D::set_rows(a, lrp, ld.t, wave, l16);
+  rp = lrp;
+  auto advance_ld = [&]() {
+    if (ld_lin < last) {
+      ++ld_lin;
+      ld.advance(GC);
+      if (ld.c == 0) D::set_rows(a, lrp, ld.t, wave, l16);
     }
-  D::store_x(a, sm, xr, 0, tid);
+  };
+
+  u32x4_t xr[NB][MT];
+  WRegs<WT, S> wr[NB];
+#pragma unroll
+  for (int r = 0; r < NB; ++r) {
+    D::load_x(a, xr[r], ld.c, tid);
+    D::load_w(a, wr[r], lrp, ld.c, h);
+    advance_ld();
+  }
+  D::store_x(a, sm, xr[0], 0, tid);
   __syncthreads();
 
-  f32x4_t acc[S][MT];
+  int j = 0;  // units done
+  int64_t batch = b0;
+  while (batch < b1) {
+    const int t = cur.t;
+    int64_t seg_end = (static_cast<int64_t>(t) + 1) * a.G;
+    if (seg_end > b1) seg_end = b1;
+    f32x4_t acc[S][MT];
 #pragma unroll
-  for (int s = 0; s < S; ++s)
+    for (int s = 0; s < S; ++s)
 #pragma unroll
-    for (int i = 0; i < MT; ++i) acc[s][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  for (int jb = 0; jb < n_units; jb += NBUF) {
+      for (int i = 0; i < MT; ++i) acc[s][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (; batch < seg_end; ++batch) {
 #pragma unroll
-    for (int r = 0; r < NBUF; ++r) {
-      const int j = jb + r;
-      if (j < n_units) {
+      for (int r = 0; r < NB; ++r, ++j) {
         const int b = j & 1;
-        const bool more = j + 1 < n_units;
-        Cursor nxt = cur;
-        nxt.advance(a.G);
-        if (more) D::load_x(a, xr, nxt.c, tid);
-        D::compute(sm, b, wr[r], acc, l16, h);
-        if (j + NBUF < n_units) {
-          D::load_w(a, wr[r], ld.t, ld.c, wave, l16, h);
-          ld.advance(a.G);
-        }
-        if (cur.c == a.G - 1 || !more) {
-          D::finish_tile(a, sm, acc, cur.t, p, u0, u1, tid);
-#pragma unroll
-          for (int s = 0; s < S; ++s)
-#pragma unroll
-            for (int i = 0; i < MT; ++i) acc[s][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        }
-        if (more) D::store_x(a, sm, xr, b ^ 1, tid);
+        D::load_x(a, xr[r], ld.c, tid);  // refill slot r with unit j + NB
+        D::compute(sm, b, wr[r], rp, acc, l16, h, nib_mask, magic);
+        D::load_w(a, wr[r], lrp, ld.c, h);
+        advance_ld();
+        // X of unit j+1 (slot r+1) into the other buffer; after the range's
+        // last unit this writes a buffer nobody reads.
+        D::store_x(a, sm, xr[(r + 1) % NB], b ^ 1, tid);
         __syncthreads();
-        cur = nxt;
+        cur.advance(GC);
       }
     }
+    D::finish_tile(a, sm, acc, t, p, b0, b1, tid);
+    if (cur.c == 0) D::set_rows(a, rp, cur.t, wave, l16);
   }
 }
 
 // Host-side launcher; returns hipError_t.
 template <int WT, int SDT, int MT, int S>
-static hipError_t launch_decode_t(const GemmArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((qgemm_decode_kernel<WT, SDT, MT, S, 3>), dim3(a.P), dim3(DEC_THREADS), 0, stream, a);
+static hipError_t launch_decode_t(const GemmArgs& a, bool kfull, hipStream_t stream) {
+  if (a.NB == 4 && kfull)
+    hipLaunchKernelGGL((qgemm_decode_kernel<WT, SDT, MT, S, 4, true>), dim3(a.P), dim3(DEC_THREADS), 0, stream, a);
+  else if (a.NB == 1)
+    hipLaunchKernelGGL((qgemm_decode_kernel<WT, SDT, MT, S, 1, false>), dim3(a.P), dim3(DEC_THREADS), 0, stream, a);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 int decode_slot_floats(int MT, int S) { return 4 * S * MT * 4 * 64; }
 
 template <int WT, int SDT>
-static hipError_t launch_decode_wt(const GemmArgs& a, int MT, int S, hipStream_t stream) {
+static hipError_t launch_decode_wt(const GemmArgs& a, int MT, int S, bool kfull, hipStream_t stream) {
 #define HSQ_DEC(mt, s) \
-  if (MT == mt && S == s) return launch_decode_t<WT, SDT, mt, s>(a, stream);
+  if (MT == mt && S == s) return launch_decode_t<WT, SDT, mt, s>(a, kfull, stream);
   HSQ_DEC(1, 1) HSQ_DEC(1, 2) HSQ_DEC(1, 4)
   HSQ_DEC(2, 1) HSQ_DEC(2, 2)
   HSQ_DEC(4, 1) HSQ_DEC(4, 2)
@@ -391,15 +459,20 @@ static hipError_t launch_decode_wt(const GemmArgs& a, int MT, int S, hipStream_t
   return hipErrorInvalidValue;
 }
 
+// The KFULL path needs K % 128 == 0 and 16-byte aligned X and W rows, and the
+// host plans it with NB = 4 chunks per stream-K step.
+bool decode_kfull(int K, int xvec, int wvec) { return (K % 128 == 0) && xvec && wvec && ((K / 128) % 4 == 0); }
+
 hipError_t launch_decode(int wt, const GemmArgs& a, int MT, int S, hipStream_t stream) {
+  const bool kfull = decode_kfull(a.K, a.xvec, a.wvec);
   if (wt == W_INT4) {
-    if (a.sdt == SCALE_BF16) return launch_decode_wt<W_INT4, SCALE_BF16>(a, MT, S, stream);
-    if (a.sdt == SCALE_F16) return launch_decode_wt<W_INT4, SCALE_F16>(a, MT, S, stream);
-    return launch_decode_wt<W_INT4, SCALE_F32>(a, MT, S, stream);
+    if (a.sdt == SCALE_BF16) return launch_decode_wt<W_INT4, SCALE_BF16>(a, MT, S, kfull, stream);
+    if (a.sdt == SCALE_F16) return launch_decode_wt<W_INT4, SCALE_F16>(a, MT, S, kfull, stream);
+    return launch_decode_wt<W_INT4, SCALE_F32>(a, MT, S, kfull, stream);
   }
-  if (a.sdt == SCALE_BF16) return launch_decode_wt<W_FP8, SCALE_BF16>(a, MT, S, stream);
-  if (a.sdt == SCALE_F16) return launch_decode_wt<W_FP8, SCALE_F16>(a, MT, S, stream);
-  return launch_decode_wt<W_FP8, SCALE_F32>(a, MT, S, stream);
+  if (a.sdt == SCALE_BF16) return launch_decode_wt<W_FP8, SCALE_BF16>(a, MT, S, kfull, stream);
+  if (a.sdt == SCALE_F16) return launch_decode_wt<W_FP8, SCALE_F16>(a, MT, S, kfull, stream);
+  return launch_decode_wt<W_FP8, SCALE_F32>(a, MT, S, kfull, stream);
 }
 
 }  // namespace hsq
