@@ -185,6 +185,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=6)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", metavar="KIND:SHAPE:M",
+                    help="eager launches of one GEMM (e.g. int4:gate_up:64) plus a plain copy kernel of "
+                    "known size, for rocprofv3 counter passes; prints one JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the quantized GEMM path has no multi-GPU mode in this build "
@@ -202,6 +205,10 @@ def main():
     _native.lib()
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev).manual_seed(0)
+
+    if args.profile:
+        profile(torch, gen, dev, args.profile, max(args.steps, 1))
+        return
 
     # ---- headline: config 1 ------------------------------------------------
     ms_list = [1, 4, 16, 64]
@@ -281,6 +288,33 @@ def main():
     if args.sweep and os.path.isdir("gpurun_out"):
         with open("gpurun_out/bench_sweep.json", "w") as f:
             json.dump(result, f, indent=1)
+
+
+SHAPES = {"gate_up": GATE_UP, "down": DOWN, "c0": C0, "qkv": QKV, "o_proj": O_PROJ, "gdn_in": GDN_IN}
+COPY_CAL_BYTES = 512 << 20
+
+
+def profile(torch, gen, dev, spec, launches):
+    """One GEMM launched eagerly `launches` times over rotated weight copies, then a
+    512 MiB device-to-device copy launched 4 times.  Under rocprofv3 --pmc the copy's
+    FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters against known bytes."""
+    kind, name, m = spec.split(":")
+    n, k = SHAPES[name]
+    m = int(m)
+    make = make_int4 if kind == "int4" else make_fp8
+    per_copy = int4_bytes(n, k) if kind == "int4" else fp8_bytes(n, k)
+    ws = make(torch, n, k, copies_for(per_copy), gen, dev)
+    x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
+    c = Case(kind, name, n, k, m, ws, x)
+    for i in range(launches):
+        c.call(i)
+    src = torch.empty(COPY_CAL_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": spec, "launches": launches, "weight_bytes_per_launch": c.wbytes,
+                      "copy_bytes_per_launch": COPY_CAL_BYTES}), flush=True)
 
 
 def sweep(torch, gen, dev):

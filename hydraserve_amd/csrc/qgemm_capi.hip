@@ -22,6 +22,12 @@ int stream_slot_floats(int MT, int S);
 bool stream_ok(const GemmArgs& a, int wt, int NB);
 bool decode_kfull(int K, int xvec, int wvec);
 int prefill_slot_floats(int BM);
+bool rows_ok(const GemmArgs& a, int wt, int P, int* nblk_out, bool* xl_out, int xl_pref);
+hipError_t launch_rows(int wt, const GemmArgs& a, int nblk, bool xl, hipStream_t stream);
+extern int rows_kw8;
+bool gemv_ok(const GemmArgs& a, int wt, int P, int kw_pref, int* kw_out, int* rows_max);
+hipError_t launch_gemv(int wt, const GemmArgs& a, int kw, hipStream_t stream);
+extern int gemv_rd;
 hipError_t launch_int4_dequant(const uint32_t* packed, int64_t ldw, const void* scale, int64_t lds, int sdt,
                                const int32_t* zero, int64_t ldz, void* out, int64_t ldo, int odt, int N, int K,
                                int group, hipStream_t stream);
@@ -38,6 +44,12 @@ constexpr int64_t kMaxTiles = 1 << 18;
 constexpr int64_t kCounterBytes = kMaxTiles * 4;
 
 struct Tuning {
+  int rows_off = 0;        // 1: never use the row-partitioned decode kernel
+  int rows_wg = 0;         // its workgroups per CU (0 = 1)
+  int rows_xl = 1;         // 0: never stage X in LDS (read A fragments from global memory)
+  int gemv_off = 0;        // 1: never use the block-major kernel
+  int gemv_kw = 0;         // its wavefronts per workgroup (0 = 8)
+  int gemv_wg = 0;         // its workgroups per CU (0 = 1)
   int st_off = 0;          // 1: never use the streaming decode kernel
   int st_s = 0;            // its strips of 16 rows per wave (0 = heuristic)
   int st_wg = 0;           // its workgroups per CU
@@ -57,6 +69,14 @@ int env_int(const char* name) {
 const Tuning& tuning() {
   static Tuning t = [] {
     Tuning r;
+    r.rows_off = env_int("HS_ROWS_OFF");
+    r.rows_wg = env_int("HS_ROWS_WG");
+    if (std::getenv("HS_ROWS_XL") != nullptr) r.rows_xl = env_int("HS_ROWS_XL");
+    rows_kw8 = env_int("HS_ROWS_KW8");
+    r.gemv_off = env_int("HS_GEMV_OFF");
+    r.gemv_kw = env_int("HS_GEMV_KW");
+    r.gemv_wg = env_int("HS_GEMV_WG");
+    gemv_rd = env_int("HS_GEMV_RD");
     r.st_off = env_int("HS_ST_OFF");
     r.st_s = env_int("HS_ST_S");
     r.st_wg = env_int("HS_ST_WG");
@@ -160,6 +180,30 @@ bool valid_dt(int dt) { return dt == HS_DT_BF16 || dt == HS_DT_F16 || dt == HS_D
 int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   a.xvec = aligned16(a.x) && (a.ldx % 8 == 0);
   const Tuning& tn = tuning();
+  // Decode with at most 16 activation rows: row-partitioned kernels, one
+  // partition per workgroup, no workspace.  Block-major when X fits in LDS.
+  if (!tn.gemv_off && a.M <= 16) {
+    const int P = device_cus() * (tn.gemv_wg > 0 ? tn.gemv_wg : 1);
+    int kw = 0, rows_max = 0;
+    if (gemv_ok(a, wt, P, tn.gemv_kw > 0 ? tn.gemv_kw : 8, &kw, &rows_max)) {
+      a.P = P;
+      a.T = a.K / 128;
+      a.G = rows_max;
+      return hip_code(launch_gemv(wt, a, kw, stream));
+    }
+  }
+  if (!tn.rows_off && a.M <= 16) {
+    const int P = device_cus() * (tn.rows_wg > 0 ? tn.rows_wg : 1);
+    int nblk = 0;
+    bool xl = false;
+    // Above 4 rows with narrow partitions (1-2 blocks of 16 weight rows per
+    // workgroup) the streaming kernel below is faster.
+    if (rows_ok(a, wt, P, &nblk, &xl, tn.rows_xl) && (a.M <= 4 || nblk >= 3)) {
+      a.P = P;
+      a.T = a.K / 128;
+      return hip_code(launch_rows(wt, a, nblk, xl, stream));
+    }
+  }
   const int nb = tn.st_nb > 0 ? tn.st_nb : stream_nb(a.M);
   const Plan p = make_plan(a.M, a.N, a.K, decode_kfull(a.K, a.xvec, a.wvec), stream_ok(a, wt, nb));
   if (p.T > kMaxTiles) return HS_EUNSUPPORTED;

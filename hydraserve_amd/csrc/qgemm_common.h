@@ -131,7 +131,7 @@ __device__ __forceinline__ float load_partial(const float* p) {
 // Count this workgroup's arrival at tile t once every thread's partial stores
 // are acknowledged; true in every thread of the workgroup that arrived last.
 __device__ __forceinline__ bool arrive_last(int* counters, int t, int contributors, int* lds_flag) {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every partial store acknowledged
   __syncthreads();
   if (threadIdx.x == 0) {
     const int old = __hip_atomic_fetch_add(&counters[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
