@@ -121,7 +121,7 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int stream_nb(int M) { return M <= 16 ? 8 : (M <= 32 ? 4 : 2); }
 
 // `fast`: the streaming kernel can run this problem (see stream_ok).
-Plan make_plan(int M, int N, int K, bool kfull, bool fast) {
+Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast) {
   Plan p;
   const int cus = device_cus();
   const Tuning& tn = tuning();
@@ -129,7 +129,10 @@ Plan make_plan(int M, int N, int K, bool kfull, bool fast) {
     p.stream = true;
     p.MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     int S = tn.st_s;
-    if (S != 1 && S != 2) S = 1;
+    // Two 16-row strips per wave halve the activation re-reads from LDS; that
+    // pays for INT4 above 16 rows on wide outputs (measured: 34816x5120 at 64
+    // rows 147 -> 109 us) and loses for FP8 and for narrow outputs.
+    if (S != 1 && S != 2) S = (wt == W_INT4 && M > 16 && N >= 2 * K) ? 2 : 1;
     p.S = S;
     p.NB = tn.st_nb > 0 ? tn.st_nb : stream_nb(M);
     p.T = static_cast<int>(cdiv(N, 64 * S));
@@ -156,7 +159,7 @@ Plan make_plan(int M, int N, int K, bool kfull, bool fast) {
   } else {
     p.decode = false;
     int bm = tn.prefill_bm;
-    if (bm != 128 && bm != 256) bm = 128;
+    if (bm != 64 && bm != 128 && bm != 256) bm = 128;
     p.BM = bm;
     p.TM = static_cast<int>(cdiv(M, bm));
     p.T = p.TM * static_cast<int>(cdiv(N, 256));
@@ -205,7 +208,7 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
     }
   }
   const int nb = tn.st_nb > 0 ? tn.st_nb : stream_nb(a.M);
-  const Plan p = make_plan(a.M, a.N, a.K, decode_kfull(a.K, a.xvec, a.wvec), stream_ok(a, wt, nb));
+  const Plan p = make_plan(wt, a.M, a.N, a.K, decode_kfull(a.K, a.xvec, a.wvec), stream_ok(a, wt, nb));
   if (p.T > kMaxTiles) return HS_EUNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < p.ws_bytes) return HS_EWORKSPACE;
   a.G = p.G;
@@ -247,7 +250,7 @@ int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
   int64_t best = 0;
   for (int kfull = 0; kfull < 2; ++kfull)
     for (int fast = 0; fast < 2; ++fast) {
-      const int64_t b = hsq::make_plan(M, N, K, kfull != 0, fast != 0).ws_bytes;
+      const int64_t b = hsq::make_plan(kind, M, N, K, kfull != 0, fast != 0).ws_bytes;
       best = b > best ? b : best;
     }
   return best;

@@ -347,6 +347,7 @@ int prefill_slot_floats(int BM) { return 4 * (BM / 32) * 2 * 16 * 64; }
 
 template <int WT, int SDT>
 static hipError_t launch_prefill_wt(const GemmArgs& a, int BM, hipStream_t stream) {
+  if (BM == 64) return launch_prefill_t<WT, SDT, 64>(a, stream);
   if (BM == 128) return launch_prefill_t<WT, SDT, 128>(a, stream);
   if (BM == 256) return launch_prefill_t<WT, SDT, 256>(a, stream);
   return hipErrorInvalidValue;
