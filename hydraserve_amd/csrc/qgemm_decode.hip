@@ -300,9 +300,11 @@ struct Decode {
   }
 
   static constexpr int SLOT = 4 * S * MT * 4 * 64;  // floats per partial slot
-  // Partial layout: f32x4 at ((wave*S + s)*MT + i)*64 + lane (16 B per lane).
+  // Partial layout: element e of block (wave, s, i) of a lane at
+  // (((wave*S + s)*MT + i)*4 + e)*64 + lane, so each store or load
+  // instruction covers 256 contiguous bytes.
   static __device__ __forceinline__ int64_t part_off(int wave, int s, int i, int lane) {
-    return ((static_cast<int64_t>(wave * S + s) * MT + i) * 64 + lane) * 4;
+    return (static_cast<int64_t>(wave * S + s) * MT + i) * 256 + lane;
   }
 
   static __device__ __forceinline__ float* slot_ptr(const GemmArgs& a, int p, int slot) {
@@ -324,7 +326,7 @@ struct Decode {
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) store_partial(mine + part_off(wave, s, i, lane) + e, acc[s][i][e]);
+        for (int e = 0; e < 4; ++e) store_partial(mine + part_off(wave, s, i, lane) + e * 64, acc[s][i][e]);
     if (!arrive_last(a.counters, t, pl - pf + 1, &sm.flag)) return;
     // Sum every contributor's slot (our own included) in workgroup order.
 #pragma unroll
@@ -338,7 +340,7 @@ struct Decode {
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[s][i][e] += load_partial(src + part_off(wave, s, i, lane) + e);
+          for (int e = 0; e < 4; ++e) acc[s][i][e] += load_partial(src + part_off(wave, s, i, lane) + e * 64);
     }
     store_tile(a, acc, t, wave, l16, h);
     reset_counter(a.counters, t);

@@ -215,10 +215,11 @@ struct Prefill {
   }
 
   static constexpr int SLOT = 4 * MI * 2 * 16 * 64;
-  // Partial layout: the 16 floats of block (i, j) of a lane are contiguous at
-  // (((wave*MI + i)*2 + j)*64 + lane)*16.
+  // Partial layout: element e of block (i, j) of a lane at
+  // ((((wave*MI + i)*2 + j)*16 + e)*64 + lane, so each store or load
+  // instruction covers 256 contiguous bytes.
   static __device__ __forceinline__ int64_t part_off(int wave, int i, int j, int lane) {
-    return ((static_cast<int64_t>(wave * MI + i) * 2 + j) * 64 + lane) * 16;
+    return (static_cast<int64_t>(wave * MI + i) * 2 + j) * 1024 + lane;
   }
 
   static __device__ __forceinline__ float* slot_ptr(const GemmArgs& a, int p, int slot) {
@@ -241,7 +242,7 @@ struct Prefill {
       for (int j = 0; j < 2; ++j) {
         float* dst = mine + part_off(wave, i, j, lane);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) store_partial(dst + e, acc[i][j][e]);
+        for (int e = 0; e < 16; ++e) store_partial(dst + e * 64, acc[i][j][e]);
         __builtin_amdgcn_sched_barrier(0);
       }
     if (!arrive_last(a.counters, t, pl - pf + 1, &sm.flag)) return;
@@ -256,7 +257,7 @@ struct Prefill {
         for (int j = 0; j < 2; ++j) {
           const float* sp = src + part_off(wave, i, j, lane);
 #pragma unroll
-          for (int e = 0; e < 16; ++e) acc[i][j][e] += load_partial(sp + e);
+          for (int e = 0; e < 16; ++e) acc[i][j][e] += load_partial(sp + e * 64);
           __builtin_amdgcn_sched_barrier(0);
         }
     }

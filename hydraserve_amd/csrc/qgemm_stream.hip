@@ -390,8 +390,11 @@ struct Stream {
   static __device__ __forceinline__ float* slot_ptr(const GemmArgs& a, int p, int slot) {
     return a.partials + (static_cast<int64_t>(p) * 2 + slot) * SLOT;
   }
+  // Element e of block (wave, s, i) of a lane sits at
+  // (((wave*S + s)*MT + i)*4 + e)*64 + lane: each store or load instruction
+  // covers 256 contiguous bytes.
   static __device__ __forceinline__ int part_off(int wave, int s, int i, int lane) {
-    return (((wave * S + s) * MT + i) * 64 + lane) * 4;
+    return ((wave * S + s) * MT + i) * 256 + lane;
   }
 
   // End of tile t inside this workgroup's range.  A tile the range covers
@@ -412,7 +415,7 @@ struct Stream {
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) store_partial(mine + part_off(wave, s, i, lane) + e, acc[s][i][e]);
+        for (int e = 0; e < 4; ++e) store_partial(mine + part_off(wave, s, i, lane) + e * 64, acc[s][i][e]);
     return true;
   }
 
@@ -465,7 +468,7 @@ struct Stream {
 #pragma unroll
             for (int i = 0; i < MT; ++i)
 #pragma unroll
-              for (int e = 0; e < 4; ++e) v[dq][s][i][e] = load_partial(src + part_off(wave, s, i, lane) + e);
+              for (int e = 0; e < 4; ++e) v[dq][s][i][e] = load_partial(src + part_off(wave, s, i, lane) + e * 64);
         }
 #pragma unroll
         for (int dq = 0; dq < 4; ++dq) {
