@@ -129,10 +129,11 @@ Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast) {
     p.stream = true;
     p.MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     int S = tn.st_s;
-    // Two 16-row strips per wave halve the activation re-reads from LDS; that
-    // pays for INT4 above 16 rows on wide outputs (measured: 34816x5120 at 64
-    // rows 147 -> 109 us) and loses for FP8 and for narrow outputs.
-    if (S != 1 && S != 2) S = (wt == W_INT4 && M > 16 && N >= 2 * K) ? 2 : 1;
+    // Above 16 rows, two 16-row strips per wave halve the activation re-reads
+    // from LDS (measured INT4 34816x5120 at 64 rows: 137 -> 94 us); only FP8
+    // on narrow outputs at up to 32 rows keeps one strip (31 vs 35 us).
+    if (S != 1 && S != 2)
+      S = (M > 16 && (wt == W_INT4 || M > 32 || N >= 2 * K)) ? 2 : 1;
     p.S = S;
     p.NB = tn.st_nb > 0 ? tn.st_nb : stream_nb(M);
     p.T = static_cast<int>(cdiv(N, 64 * S));
