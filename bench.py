@@ -81,6 +81,21 @@ def make_fp8(torch, n, k, copies, gen, dev):
     return out
 
 
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of
+# `bench.py --profile KIND:SHAPE:M` (KiB per dispatch), scaled by what the same
+# counters read for a 512 MiB copy: FETCH x2.0, WRITE x1.0.  Kept beside the
+# summaries under profiles/; shapes not listed report null.
+PMC_TRAFFIC_KIB = {("int4", "gate_up", 64): (60180.5, 19728.5)}
+FETCH_CAL, WRITE_CAL = 2.0, 1.0
+
+
+def pmc_traffic(kind, name, m):
+    kib = PMC_TRAFFIC_KIB.get((kind, name, m))
+    if kib is None:
+        return None
+    return int((kib[0] * FETCH_CAL + kib[1] * WRITE_CAL) * 1024)
+
+
 def graph_time_ms(torch, fn, reps, inner):
     """Capture `inner` calls of fn(i) in one graph, replay `reps` times; ms per call."""
     s = torch.cuda.Stream()
@@ -247,7 +262,7 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(dom_r["weight_GBps"] / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": pmc_traffic("int4", dom_c.name, dom_c.m),
         "kernel": f"INT4 decode {dom_c.name} M={dom_c.m} ({dom_c.n}x{dom_c.k})",
         "bytes_per_launch": dom_c.wbytes,
         "us_per_launch": dom_r["us"],
