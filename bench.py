@@ -19,8 +19,8 @@ duration (events around graph replays of back-to-back launches of that GEMM).
 oracle/torch_cpu_path.py) timed on a bounded sample on the host cores.
 
 --sweep additionally measures every BASELINE config (INT4/FP8, decode and
-prefill, the config-4 layer) and prints one JSON object per shape to stderr
-and to gpurun_out/bench_sweep.json when that directory exists.
+prefill, the config-4 layer) and prints one JSON object per shape to stderr;
+--sweep-json PATH also writes the whole result there.
 """
 
 from __future__ import annotations
@@ -200,13 +200,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=6)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep-json", metavar="PATH", help="with --sweep: also write the result to PATH")
     ap.add_argument("--profile", metavar="KIND:SHAPE:M",
                     help="eager launches of one GEMM (e.g. int4:gate_up:64) plus a plain copy kernel of "
                     "known size, for rocprofv3 counter passes; prints one JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the quantized GEMM path has no multi-GPU mode in this build "
-              "(column/row sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "(column-parallel along N needs no communication, row-parallel along K one all-reduce of Y); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -300,8 +301,8 @@ def main():
     if args.sweep:
         result["sweep"] = sweep(torch, gen, dev)
     print(json.dumps(result), flush=True)
-    if args.sweep and os.path.isdir("gpurun_out"):
-        with open("gpurun_out/bench_sweep.json", "w") as f:
+    if args.sweep and args.sweep_json:
+        with open(args.sweep_json, "w") as f:
             json.dump(result, f, indent=1)
 
 

@@ -141,8 +141,8 @@ __global__ __launch_bounds__(64 * KW) void qgemm_gemv_kernel(GemmArgs a) {
 
   // ---- staging: X (16-byte units; INT4 permuted to int4_operand's order, with
   // the fp32 group sums computed on the way), scales and zero points (dword
-  // units, or 16-bit when a scale row is not dword-aligned).  Every round
-  // issues all of its loads before storing; round 0 is issued before the
+  // units, or 16-bit when a scale row is not dword-aligned).  Every pass
+  // issues all of its loads before storing; pass 0 is issued before the
   // first weight loads so waiting for it never waits for those.
   const int xupr = a.K / 8;                 // 16-byte X units per row (multiple of 16)
   const int xunits = M * xupr;
