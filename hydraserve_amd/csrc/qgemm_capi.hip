@@ -22,6 +22,9 @@ int stream_slot_floats(int MT, int S);
 bool stream_ok(const GemmArgs& a, int wt, int NB);
 bool decode_kfull(int K, int xvec, int wvec);
 int prefill_slot_floats(int BM);
+hipError_t launch_wide(int wt, const GemmArgs& a, hipStream_t stream);
+int wide_slot_floats();
+bool wide_ok(const GemmArgs& a, int wt);
 bool rows_ok(const GemmArgs& a, int wt, int P, int* nblk_out, bool* xl_out, int xl_pref);
 hipError_t launch_rows(int wt, const GemmArgs& a, int nblk, bool xl, hipStream_t stream);
 extern int rows_kw8;
@@ -57,6 +60,8 @@ struct Tuning {
   int decode_s = 0;        // strips of 16 rows per wave (0 = heuristic)
   int decode_wg_per_cu = 0;
   int prefill_bm = 0;
+  int wide_off = 0;         // 1: never use the 256x256-tile prefill kernel
+  int wide_min_m = 0;      // smallest M for it (0 = 256)
   int prefill_wg_per_cu = 0;
 };
 
@@ -84,6 +89,8 @@ const Tuning& tuning() {
     r.decode_s = env_int("HS_DECODE_S");
     r.decode_wg_per_cu = env_int("HS_DECODE_WG_PER_CU");
     r.prefill_bm = env_int("HS_PREFILL_BM");
+    r.wide_off = env_int("HS_WIDE_OFF");
+    r.wide_min_m = env_int("HS_WIDE_MIN_M");
     r.prefill_wg_per_cu = env_int("HS_PREFILL_WG_PER_CU");
     return r;
   }();
@@ -107,6 +114,7 @@ int device_cus() {
 struct Plan {
   bool stream = false;  // streaming decode kernel (fast path)
   bool decode = true;
+  bool wide = false;    // 256x256-tile prefill kernel
   int MT = 1, S = 1, BM = 256, NB = 1;
   int T = 0, TM = 1, G = 0;
   int64_t U = 0;
@@ -120,8 +128,9 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 int stream_nb(int M) { return M <= 16 ? 8 : (M <= 32 ? 4 : 2); }
 
-// `fast`: the streaming kernel can run this problem (see stream_ok).
-Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast) {
+// `fast`: the streaming kernel can run this problem (see stream_ok); `wide`:
+// the 256x256-tile prefill kernel can (see wide_ok).
+Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast, bool wide) {
   Plan p;
   const int cus = device_cus();
   const Tuning& tn = tuning();
@@ -157,6 +166,20 @@ Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast) {
     p.U = static_cast<int64_t>(p.T) * p.G;
     p.P = static_cast<int>(p.U < static_cast<int64_t>(cus) * occ ? p.U : static_cast<int64_t>(cus) * occ);
     p.slot_floats = decode_slot_floats(p.MT, p.S);
+  } else if (wide && !tn.wide_off && M >= (tn.wide_min_m > 0 ? tn.wide_min_m : 256) &&
+             2 * cdiv(M, 256) * cdiv(N, 256) >= cus) {
+    // 256x256 tiles need about one tile per two CUs: with fewer, most tiles
+    // are split across many workgroups and their 256 KB fp32 partials cost
+    // more than the bigger tiles save (down 17408->5120 at 512 rows: 382 us
+    // vs 191 us for 128-row tiles).
+    p.decode = false;
+    p.wide = true;
+    p.TM = static_cast<int>(cdiv(M, 256));
+    p.T = p.TM * static_cast<int>(cdiv(N, 256));
+    p.G = K / 64;
+    p.U = static_cast<int64_t>(p.T) * p.G;
+    p.P = static_cast<int>(p.U < cus ? p.U : cus);
+    p.slot_floats = wide_slot_floats();
   } else {
     p.decode = false;
     int bm = tn.prefill_bm;
@@ -209,7 +232,8 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
     }
   }
   const int nb = tn.st_nb > 0 ? tn.st_nb : stream_nb(a.M);
-  const Plan p = make_plan(wt, a.M, a.N, a.K, decode_kfull(a.K, a.xvec, a.wvec), stream_ok(a, wt, nb));
+  const Plan p =
+      make_plan(wt, a.M, a.N, a.K, decode_kfull(a.K, a.xvec, a.wvec), stream_ok(a, wt, nb), wide_ok(a, wt));
   if (p.T > kMaxTiles) return HS_EUNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < p.ws_bytes) return HS_EWORKSPACE;
   a.G = p.G;
@@ -222,6 +246,7 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.counter_bytes);
   hipError_t e = p.stream   ? launch_stream(wt, a, p.MT, p.S, stream)
                  : p.decode ? launch_decode(wt, a, p.MT, p.S, stream)
+                 : p.wide   ? launch_wide(wt, a, stream)
                             : launch_prefill(wt, a, p.BM, stream);
   return hip_code(e);
 }
@@ -250,10 +275,11 @@ int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
   // The bound covers every variant the call may pick for this shape.
   int64_t best = 0;
   for (int kfull = 0; kfull < 2; ++kfull)
-    for (int fast = 0; fast < 2; ++fast) {
-      const int64_t b = hsq::make_plan(kind, M, N, K, kfull != 0, fast != 0).ws_bytes;
-      best = b > best ? b : best;
-    }
+    for (int fast = 0; fast < 2; ++fast)
+      for (int wide = 0; wide < 2; ++wide) {
+        const int64_t b = hsq::make_plan(kind, M, N, K, kfull != 0, fast != 0, wide != 0).ws_bytes;
+        best = b > best ? b : best;
+      }
   return best;
 }
 

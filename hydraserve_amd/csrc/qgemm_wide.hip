@@ -1,0 +1,480 @@
+// Prefill-regime quantized weight GEMM for gfx950: 256x256 output tiles.
+//
+// Replaces the Triton launches of hydraserve/kernels/awq.py:52-74
+// (_awq_gemm_kernel, awq.py:82-142) and hydraserve/kernels/fp8.py:68-96
+// (_fp8_gemm_kernel, fp8.py:104-168) for large M.
+//
+// Budget that shapes the kernel (measured on MI355X): a 32x32x16 bf16 MFMA
+// issues every 32 cycles per SIMD, up to ~4 independent VALU ops co-issue with
+// each one for free, and LDS serves ~100-140 B/clk per CU.  So:
+//   * a workgroup (4 wavefronts) owns a 256x256 output tile; wave w owns all
+//     256 rows and output columns [64w, 64w+64): 8x2 blocks of 32x32 fp32
+//     accumulators (256 AGPRs).  Every weight element a wave decodes feeds 8
+//     MFMA row blocks, which brings the exact dequantisation to ~2.4 VALU ops
+//     per MFMA;
+//   * K advances 64 per unit.  X tiles [256 x 64] go from global memory
+//     straight into a ring of three LDS buffers (buffer_load ... lds, two
+//     units ahead; no staging registers) and are read as A fragments by all
+//     four waves: 32 KB per wave per unit, ~80 B/clk per CU at full MFMA
+//     rate.  One barrier per unit, before its last K16 step, after which the
+//     next unit's first A fragments are read during that step;
+//   * weights stream from global memory into registers two units ahead and
+//     are dequantised one K16 step ahead of their MFMAs;
+//   * XCD-aware stream-K: workgroups are numbered so that the ones sharing an
+//     XCD (dispatch round-robins workgroups over the 8 XCDs) take one
+//     contiguous run of tiles, and tiles are numbered M-major, so an XCD's
+//     workgroups share the same 256-row X slice in their L2 while all XCDs
+//     sweep the weight columns in step (shared through the MALL).
+//
+// Dequantisation matches the reference's weight bits:
+//   INT4: bf16_rne((q - z) * s) (awq.py:18-22, awq.py:136-137).  The nibble
+//         is OR-ed under the exponent of 1024.0 in fp16 (0x6400 | q = 1024+q)
+//         and v_fma_mix_f32 computes (1024+q)*s - (1024+z)*s, exact in fp32
+//         for bf16/fp16 scales (both products have at most 22 significant
+//         bits), then v_cvt_pk_bf16_f32 rounds once.  fp32 scales take
+//         ((q - z) * s) rounded in fp32 first, as the reference does.
+//   FP8:  bf16_rne(fp32(decode(b)) * fp32(s)) (fp8.py:144-161); E4M3FN ->
+//         fp32 is exact (v_cvt_pk_f32_fp8).
+// Within a unit the K order is permuted identically for X and W: lane half h
+// of every MFMA step t takes K offsets 32h + 8t .. +8, so each lane reads one
+// contiguous 16-byte (INT4) / 32-byte (FP8) run of its weight row per unit.
+//
+// Shapes (checked on the host, wide_ok): K a multiple of 128, X and W rows
+// 16-byte aligned; M and N are free (rows past the end are clamped on load
+// and masked on store).
+
+#include "qgemm_common.h"
+#include "qgemm_ops.h"
+
+namespace hsq {
+
+constexpr int WD_THREADS = 256;
+
+template <int WT, int SDT>
+struct Wide {
+  static constexpr int BM = 256;
+  static constexpr int BN = 256;
+  static constexpr int BK = 64;
+  static constexpr int MI = BM / 32;
+  static constexpr int XB = BM * BK * 2;  // bytes of one X tile in LDS
+  static constexpr int XR = BM * BK * 2 / (1024 * 4);  // 1 KB LDS-DMA loads per wave per unit
+  static constexpr int RW = WT == W_INT4 ? 1 : 2;  // 16-byte weight loads per row per unit
+  static constexpr int SLOT = 4 * MI * 2 * 16 * 64;  // floats of one partial tile
+
+  // X ring: tile row r (128 bytes) holds its 16-byte K segment g at slot
+  // g ^ (r & 7), so the 16-byte A-fragment reads of 8 consecutive rows hit
+  // 8 distinct bank groups.
+  struct Smem {
+    __attribute__((aligned(1024))) uint8_t xs[3][XB];
+    int flag;
+  };
+
+  // Raw loads of one unit for the lane's two rows: weights, scale bits and
+  // (INT4) zero-point words.  Nothing is derived from them until they are
+  // decoded, so issuing the loads never makes the wave wait for them.
+  struct Raw {
+    u32x4_t q0[RW], q1[RW];
+    uint32_t s0, s1, z0, z1;
+  };
+
+  static __device__ __forceinline__ void coords(const GemmArgs& a, int t, int& tm, int& tn) {
+    const int tnn = a.T / a.TM;
+    tm = t / tnn;
+    tn = t - tm * tnn;
+  }
+
+  // Per-tile byte offsets of the lane's loads (buffer loads: SGPR resource,
+  // 32-bit lane offset, uniform per-unit offset).
+  struct Offs {
+    uint32_t x[XR];     // X source of the lane's 16 bytes in LDS-DMA load q
+    uint32_t w[2];      // weight row j at the lane's 16/32-byte run of a unit
+    uint32_t s[2];      // scale row j (INT4) / scale block row (FP8)
+    uint32_t z[2];      // INT4 zero-point word row of row j
+    uint32_t zsh[2];    // nibble shift of row j
+  };
+
+  static __device__ __forceinline__ void offsets(const GemmArgs& a, Offs& o, int tm, int tn, int wave, int l32,
+                                                 int h, int tid) {
+    // Load q of wave w fills LDS rows 8(4q + w) .. +8 (1 KB, lane l at byte
+    // 16 l): row 8(4q + w) + l/8, slot l%8, i.e. K segment (l%8) ^ (l/8).
+    const int lane = tid & 63;
+#pragma unroll
+    for (int q = 0; q < XR; ++q) {
+      int row = tm * BM + 8 * (4 * q + wave) + (lane >> 3);
+      row = row < a.M ? row : a.M - 1;
+      const int seg = (lane & 7) ^ (lane >> 3);
+      o.x[q] = static_cast<uint32_t>((row * a.ldx + seg * 8) * 2);
+    }
+    constexpr int SES = SDT == SCALE_F32 ? 4 : 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      int row = tn * BN + wave * 64 + 32 * j + l32;
+      row = row < a.N ? row : a.N - 1;
+      if constexpr (WT == W_INT4) {
+        o.w[j] = static_cast<uint32_t>(row * a.ldw * 4 + 16 * h);
+        o.s[j] = static_cast<uint32_t>(row * a.lds * SES);
+        o.z[j] = static_cast<uint32_t>((row >> 3) * a.ldz * 4);
+        o.zsh[j] = (row & 7) * 4;
+      } else {
+        o.w[j] = static_cast<uint32_t>(row * a.ldw + 32 * h);
+        o.s[j] = static_cast<uint32_t>((row >> 7) * a.lds * SES);
+        o.z[j] = o.zsh[j] = 0;
+      }
+    }
+  }
+
+  struct Rsrc {
+    __amdgpu_buffer_rsrc_t x, w, s, z;
+  };
+
+  static __device__ __forceinline__ void load_raw(const Rsrc& rs, const Offs& o, Raw& r, int c) {
+    const uint32_t g = static_cast<uint32_t>(c >> 1);
+    constexpr uint32_t SES = SDT == SCALE_F32 ? 4 : 2;
+    const uint32_t soff_s = __builtin_amdgcn_readfirstlane(g * SES);
+    const uint32_t soff_z = __builtin_amdgcn_readfirstlane(g * 4u);
+    const uint32_t soff_w = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c) * (WT == W_INT4 ? 32u : 64u));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      u32x4_t* dst = j == 0 ? r.q0 : r.q1;
+      uint32_t sb;
+      if constexpr (SDT == SCALE_F32) {
+        sb = bload<uint32_t>(rs.s, o.s[j], soff_s);
+      } else {
+        sb = bload<uint16_t>(rs.s, o.s[j], soff_s);
+      }
+      uint32_t zw = 0;
+      dst[0] = bload<u32x4_t>(rs.w, o.w[j], soff_w);
+      if constexpr (WT == W_INT4) {
+        zw = bload<uint32_t>(rs.z, o.z[j], soff_z);
+      } else {
+        dst[1] = bload<u32x4_t>(rs.w, o.w[j] + 16u, soff_w);
+      }
+      if (j == 0) {
+        r.s0 = sb;
+        r.z0 = zw;
+      } else {
+        r.s1 = sb;
+        r.z1 = zw;
+      }
+    }
+  }
+
+  // X rows [tm*BM, +BM), K [c*64, +64) into the LDS buffer at byte `buf`.
+  // Rows past M repeat row M-1 (finite, never stored).
+  static __device__ __forceinline__ void dma_x(const Rsrc& rs, const Offs& o, Smem& sm, int buf, int c, int wave) {
+    const uint32_t soff = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c) * 128u);
+#pragma unroll
+    for (int q = 0; q < XR; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.x, &sm.xs[0][0] + buf + 1024 * (4 * q + wave), 16, o.x[q], soff,
+                                               0, 0);
+  }
+
+  // Fragment (row half j, step t) of the next unit: 8 weights of the lane's
+  // row in K order.
+  static __device__ __forceinline__ bf16x8_t decode(const Raw& r, const uint32_t (&zsh)[2], int j, int t) {
+    u32x4_t p;
+    const u32x4_t* q = j == 0 ? r.q0 : r.q1;
+    const uint32_t sb = j == 0 ? r.s0 : r.s1;
+    float s;
+    if constexpr (SDT == SCALE_F32) {
+      s = __uint_as_float(sb);
+    } else if constexpr (SDT == SCALE_BF16) {
+      s = __uint_as_float(sb << 16);
+    } else {
+      s = __half2float(__ushort_as_half(static_cast<unsigned short>(sb)));
+    }
+    if constexpr (WT == W_INT4) {
+      // 1024 + z, and the constant of fma(1024 + q, s, c): -(1024 + z) * s
+      // (fp32 scales: 1024 + z itself, subtracted before the multiply).
+      const float zp = static_cast<float>(1024u + (((j == 0 ? r.z0 : r.z1) >> zsh[j]) & 0xFu));
+      const float c = SDT == SCALE_F32 ? zp : -(zp * s);
+      typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+      const uint32_t w = q[0][t];
+      float f[8];
+#pragma unroll
+      for (int sh = 0; sh < 4; ++sh) {
+        const f16x2_t v = __builtin_bit_cast(f16x2_t, ((w >> (4 * sh)) & 0x000F000Fu) | 0x64006400u);
+        if constexpr (SDT == SCALE_F32) {
+          f[sh] = (static_cast<float>(v[0]) - c) * s;
+          f[sh + 4] = (static_cast<float>(v[1]) - c) * s;
+        } else {
+          f[sh] = __builtin_fmaf(static_cast<float>(v[0]), s, c);
+          f[sh + 4] = __builtin_fmaf(static_cast<float>(v[1]), s, c);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
+    } else {
+      (void)zsh;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t d = q[t >> 1][(t & 1) * 2 + e];
+        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(d, false);
+        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(d, true);
+        p[2 * e] = pack_bf16x2(lo[0] * s, lo[1] * s);
+        p[2 * e + 1] = pack_bf16x2(hi[0] * s, hi[1] * s);
+      }
+    }
+    return __builtin_bit_cast(bf16x8_t, p);
+  }
+
+  // A fragment of row block i, step t: row 32i + l32, K segment 4h + t.
+  // aoff[t] = l32*128 + ((4h + t) ^ (l32 & 7))*16.
+  static __device__ __forceinline__ bf16x8_t read_a(const Smem& sm, int buf, uint32_t aoff, int i) {
+    return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(&sm.xs[0][0] + buf + aoff + 4096 * i));
+  }
+
+  // One unit: four K16 steps of 16 MFMAs (8 row blocks x 2 column blocks)
+  // on A/B fragments prepared one step ahead.  At entry A and B hold step 0
+  // of this unit (X in LDS buffer bc, raw weights Rc); at exit, step 0 of the
+  // next unit (bn, Rn).  Step 3 starts by waiting for every load in flight
+  // (the next unit's X and weights, issued one unit ago) and the workgroup
+  // barrier; then the loads of the unit after next are issued: X by LDS-DMA
+  // into bd (last read before this barrier) and its weights into Rc (last
+  // decoded during step 2).
+  static __device__ __forceinline__ void unit(Smem& sm, int bc, int bn, int bd, int cnext2, bf16x8_t (&A)[MI],
+                                              bf16x8_t (&B)[2], Raw& Rc, const Raw& Rn, const Rsrc& rs,
+                                              const Offs& o, const uint32_t (&aoff)[4], f32x16_t (&acc)[MI][2],
+                                              int wave) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (t == 3) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        dma_x(rs, o, sm, bd, cnext2, wave);
+        load_raw(rs, o, Rc, cnext2);
+      }
+      bf16x8_t An[MI], Bn[2];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) An[i] = t < 3 ? read_a(sm, bc, aoff[t + 1], i) : read_a(sm, bn, aoff[0], i);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) Bn[j] = t < 3 ? decode(Rc, o.zsh, j, t + 1) : decode(Rn, o.zsh, j, 0);
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[i], B[0], acc[i][0], 0, 0, 0);
+        acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[i], B[1], acc[i][1], 0, 0, 0);
+      }
+      // Per row block: one LDS read, two MFMAs, ~5 VALU ops.
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i) A[i] = An[i];
+      B[0] = Bn[0];
+      B[1] = Bn[1];
+    }
+  }
+
+  // Lane (l32, h), register e of block (i, j): row 32i + 8(e/4) + 4h + e%4,
+  // column 64*wave + 32j + l32.
+  static __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&acc)[MI][2], int tm,
+                                                    int tn, int wave, int l32, int h) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = tn * BN + wave * 64 + 32 * j + l32;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = tm * BM + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (m < a.M) a.y[m * a.ldy + n] = to_bf16_bits(acc[i][j][e]);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // Partial layout: element e of block (i, j) of a lane at
+  // ((((wave*MI + i)*2 + j)*16 + e)*64 + lane: every store or load
+  // instruction covers 256 contiguous bytes.
+  static __device__ __forceinline__ int64_t part_off(int wave, int i, int j, int lane) {
+    return (static_cast<int64_t>(wave * MI + i) * 2 + j) * 1024 + lane;
+  }
+
+  static __device__ __forceinline__ float* slot_ptr(const GemmArgs& a, int v, int slot) {
+    return a.partials + (static_cast<int64_t>(v) * 2 + slot) * SLOT;
+  }
+
+  static __device__ __forceinline__ void finish_tile(const GemmArgs& a, Smem& sm, f32x16_t (&acc)[MI][2], int t,
+                                                     int tm, int tn, int v, int64_t u0, int64_t u1, int tid) {
+    const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    const int64_t ts = static_cast<int64_t>(t) * a.G, te = ts + a.G;
+    if (u0 <= ts && u1 >= te) {
+      store_tile(a, acc, tm, tn, wave, l32, h);
+      return;
+    }
+    const int pf = unit_owner(ts, a.U, a.P), pl = unit_owner(te - 1, a.U, a.P);
+    float* mine = slot_ptr(a, v, partial_slot(v, t, a.G, a.U, a.P));
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float* dst = mine + part_off(wave, i, j, lane);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) store_partial(dst + e * 64, acc[i][j][e]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    if (!arrive_last(a.counters, t, pl - pf + 1, &sm.flag)) return;
+    // Sum every contributor's slot (ours included) in workgroup order, one
+    // 32x32 block at a time, and store it.
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        f32x16_t sum = {};
+        for (int q = pf; q <= pl; ++q) {
+          const float* sp = slot_ptr(a, q, partial_slot(q, t, a.G, a.U, a.P)) + part_off(wave, i, j, lane);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sum[e] += load_partial(sp + e * 64);
+        }
+        const int n = tn * BN + wave * 64 + 32 * j + l32;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = tm * BM + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (m < a.M && n < a.N) a.y[m * a.ldy + n] = to_bf16_bits(sum[e]);
+        }
+      }
+    reset_counter(a.counters, t);
+  }
+};
+
+// a.G = 64-wide K units per tile, a.T = tiles, a.TM = tiles along M,
+// a.U = T * G, a.P = workgroups.  Tile t covers rows (t / (T/TM)) * 256 and
+// weight rows (t % (T/TM)) * 256.
+template <int WT, int SDT>
+__global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
+  using W = Wide<WT, SDT>;
+  __shared__ typename W::Smem sm;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+  const int p = blockIdx.x;
+  // Workgroups of one XCD (p % 8) take one contiguous run of units.
+  const int v = (a.P % 8 == 0) ? (p % 8) * (a.P / 8) + p / 8 : p;
+  const int64_t u0 = unit_begin(v, a.U, a.P), u1 = unit_begin(v + 1, a.U, a.P);
+  // Byte extents of the buffers (wide_ok keeps them below 2^32).
+  typename W::Rsrc rs;
+  rs.x = make_rsrc(a.x, (static_cast<int64_t>(a.M - 1) * a.ldx + a.K) * 2);
+  if constexpr (WT == W_INT4) {
+    rs.w = make_rsrc(a.w, (static_cast<int64_t>(a.N - 1) * a.ldw + a.K / 8) * 4);
+    rs.z = make_rsrc(a.zero, (static_cast<int64_t>((a.N - 1) / 8) * a.ldz + a.K / 128) * 4);
+    rs.s = make_rsrc(a.scale, (static_cast<int64_t>(a.N - 1) * a.lds + a.K / 128) * (SDT == SCALE_F32 ? 4 : 2));
+  } else {
+    rs.w = make_rsrc(a.w, static_cast<int64_t>(a.N - 1) * a.ldw + a.K);
+    rs.z = rs.w;
+    rs.s = make_rsrc(a.scale, (static_cast<int64_t>((a.N - 1) / 128) * a.lds + a.K / 128) *
+                                  (SDT == SCALE_F32 ? 4 : 2));
+  }
+
+  uint32_t aoff[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) aoff[t] = l32 * 128 + (((4 * h + t) ^ (l32 & 7)) * 16);
+
+  int64_t u = u0;
+  while (u < u1) {
+    const int t = static_cast<int>(u / a.G);
+    const int cb = static_cast<int>(u - static_cast<int64_t>(t) * a.G);
+    const int ce = static_cast<int>((u1 - static_cast<int64_t>(t) * a.G) < a.G ? (u1 - static_cast<int64_t>(t) * a.G)
+                                                                                : a.G);
+    const int n = ce - cb;
+    int tm, tn;
+    W::coords(a, t, tm, tn);
+
+    // Prologue: X(cb), X(cb+1) into LDS buffers 0, 1; weights of cb and
+    // cb+1 into registers; step 0 of cb prepared.
+    typename W::Offs o;
+    W::offsets(a, o, tm, tn, wave, l32, h, tid);
+    typename W::Raw r0, r1;
+    const int c1 = cb + 1 < ce ? cb + 1 : ce - 1;
+    W::dma_x(rs, o, sm, 0, cb, wave);
+    W::dma_x(rs, o, sm, W::XB, c1, wave);
+    W::load_raw(rs, o, r0, cb);
+    W::load_raw(rs, o, r1, c1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    bf16x8_t A[W::MI], B[2];
+#pragma unroll
+    for (int i = 0; i < W::MI; ++i) A[i] = W::read_a(sm, 0, aoff[0], i);
+    B[0] = W::decode(r0, o.zsh, 0, 0);
+    B[1] = W::decode(r0, o.zsh, 1, 0);
+
+    f32x16_t acc[W::MI][2];
+#pragma unroll
+    for (int i = 0; i < W::MI; ++i) acc[i][0] = acc[i][1] = f32x16_t{};
+
+    // LDS buffers rotate b0 (this unit) -> b1 (next) -> b2 (DMA target).
+    // Unit indices past the tile's last are clamped (their loads are
+    // harmless and never used).  Units run in pairs so that the two
+    // raw-weight register sets alternate without copies, and the pair loop
+    // has a single exit (a break between the two units makes the register
+    // allocator shuffle the accumulators); an odd unit count peels one unit
+    // first and swaps the sets once.
+    int b0 = 0, b1 = W::XB, b2 = 2 * W::XB;
+    int q = 0;
+    if (n & 1) {
+      const int cn = cb + 2 < ce ? cb + 2 : ce - 1;
+      W::unit(sm, b0, b1, b2, cn, A, B, r0, r1, rs, o, aoff, acc, wave);
+      const int tb = b0;
+      b0 = b1;
+      b1 = b2;
+      b2 = tb;
+      const typename W::Raw tr = r0;
+      r0 = r1;
+      r1 = tr;
+      q = 1;
+    }
+    for (; q < n; q += 2) {
+      const int cn0 = cb + q + 2 < ce ? cb + q + 2 : ce - 1;
+      const int cn1 = cb + q + 3 < ce ? cb + q + 3 : ce - 1;
+      W::unit(sm, b0, b1, b2, cn0, A, B, r0, r1, rs, o, aoff, acc, wave);
+      W::unit(sm, b1, b2, b0, cn1, A, B, r1, r0, rs, o, aoff, acc, wave);
+      const int tb = b0;
+      b0 = b2;
+      b2 = b1;
+      b1 = tb;
+    }
+    // Drain the clamped prefetches before the buffers are reused.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    W::finish_tile(a, sm, acc, t, tm, tn, v, u0, u1, tid);
+    __syncthreads();
+    u += n;
+  }
+}
+
+template <int WT, int SDT>
+static hipError_t launch_wide_t(const GemmArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((qgemm_wide_kernel<WT, SDT>), dim3(a.P), dim3(WD_THREADS), 0, stream, a);
+  return hipGetLastError();
+}
+
+int wide_slot_floats() { return Wide<W_INT4, SCALE_BF16>::SLOT; }
+
+bool wide_ok(const GemmArgs& a, int wt) {
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % 128 != 0 || !a.xvec || !a.wvec) return false;
+  // Every buffer-load byte offset must fit in 32 bits.
+  const int64_t lim = int64_t(1) << 31;
+  const int64_t xb = (static_cast<int64_t>(a.M) * a.ldx + a.K) * 2;
+  const int64_t wb = wt == W_INT4 ? (static_cast<int64_t>(a.N) * a.ldw + a.K / 8) * 4
+                                  : static_cast<int64_t>(a.N) * a.ldw + a.K;
+  const int64_t sb = (static_cast<int64_t>(a.N) * a.lds + a.K / 128) * 4;
+  const int64_t zb = (static_cast<int64_t>(a.N / 8 + 1) * a.ldz + a.K / 128) * 4;
+  return xb < lim && wb < lim && sb < lim && zb < lim;
+}
+
+hipError_t launch_wide(int wt, const GemmArgs& a, hipStream_t stream) {
+  if (wt == W_INT4) {
+    if (a.sdt == SCALE_BF16) return launch_wide_t<W_INT4, SCALE_BF16>(a, stream);
+    if (a.sdt == SCALE_F16) return launch_wide_t<W_INT4, SCALE_F16>(a, stream);
+    return launch_wide_t<W_INT4, SCALE_F32>(a, stream);
+  }
+  if (a.sdt == SCALE_BF16) return launch_wide_t<W_FP8, SCALE_BF16>(a, stream);
+  if (a.sdt == SCALE_F16) return launch_wide_t<W_FP8, SCALE_F16>(a, stream);
+  return launch_wide_t<W_FP8, SCALE_F32>(a, stream);
+}
+
+}  // namespace hsq

@@ -239,6 +239,32 @@ def test_int4_stream_k_many_contributors(m):
     assert_gemm_close(y1, int4_ref(x_bits, packed, scale, zero, n, k))
 
 
+WIDE_SHAPES = [(256, 256, 128), (300, 520, 1024), (513, 264, 640), (260, 300, 2176), (257, 1000, 384)]
+
+
+@pytest.mark.parametrize("m,n,k", WIDE_SHAPES)
+def test_int4_wide_tiles(m, n, k):
+    # M >= 256 with K % 128 == 0 takes the 256x256-tile kernel: ragged M and N
+    # tails, even and odd unit counts per workgroup range, tiles split across
+    # many stream-K contributors (few tiles, up to one unit per workgroup).
+    dev = _cuda()
+    rng = np.random.default_rng(m + 3 * n + 7 * k)
+    w, x, x_bits, packed, scale, zero, _ = int4_case(rng, m, n, k, dev)
+    y1 = hs.awq_linear(x, w)
+    y2 = hs.awq_linear(x, w)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert_gemm_close(y1, int4_ref(x_bits, packed, scale, zero, n, k), what=f"{m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("sdt", [torch.float16, torch.float32])
+def test_int4_wide_tiles_other_scale_dtypes(sdt):
+    dev = _cuda()
+    rng = np.random.default_rng(17)
+    m, n, k = 300, 264, 640
+    w, x, x_bits, packed, scale, zero, _ = int4_case(rng, m, n, k, dev, sdt)
+    assert_gemm_close(hs.awq_linear(x, w), int4_ref(x_bits, packed, scale, zero, n, k))
+
+
 def test_int4_batched_shape_and_empty():
     dev = _cuda()
     rng = np.random.default_rng(9)
@@ -360,6 +386,17 @@ def test_fp8_stream_k_many_contributors(m):
     y2 = hs.fp8_linear(x, w)
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
     assert_gemm_close(y1, fp8_ref(xb, data, scale, n, k))
+
+
+@pytest.mark.parametrize("m,n,k", WIDE_SHAPES)
+def test_fp8_wide_tiles(m, n, k):
+    dev = _cuda()
+    rng = np.random.default_rng(5 * m + n + k)
+    w, x, xb, data, scale = fp8_case(rng, m, n, k, dev)
+    y1 = hs.fp8_linear(x, w)
+    y2 = hs.fp8_linear(x, w)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert_gemm_close(y1, fp8_ref(xb, data, scale, n, k), what=f"{m}x{n}x{k}")
 
 
 def test_fp8_streams_host_resident_weight():
