@@ -23,6 +23,9 @@ bool stream_ok(const GemmArgs& a, int wt, int NB);
 bool decode_kfull(int K, int xvec, int wvec);
 int prefill_slot_floats(int BM);
 hipError_t launch_wide(int wt, const GemmArgs& a, hipStream_t stream);
+hipError_t launch_mid(int wt, const GemmArgs& a, int bmi, int nj, hipStream_t stream);
+int mid_slot_floats(int bmi, int nj);
+bool mid_ok(const GemmArgs& a, int wt);
 int wide_slot_floats();
 bool wide_ok(const GemmArgs& a, int wt);
 bool rows_ok(const GemmArgs& a, int wt, int P, int* nblk_out, bool* xl_out, int xl_pref);
@@ -62,6 +65,10 @@ struct Tuning {
   int prefill_bm = 0;
   int wide_off = 0;         // 1: never use the 256x256-tile prefill kernel
   int wide_min_m = 0;      // smallest M for it (0 = 256)
+  int tune = 0;            // GemmArgs::tune experiment bits
+  int mid_off = 0;         // 1: never use the LDS-DMA streaming kernel for 17..64 rows
+  int mid_min_m = 0;       // smallest M for it (0 = 17)
+  int mid_nj = 0;          // its 32-column blocks per wave (0 = heuristic)
   int prefill_wg_per_cu = 0;
 };
 
@@ -91,6 +98,10 @@ const Tuning& tuning() {
     r.prefill_bm = env_int("HS_PREFILL_BM");
     r.wide_off = env_int("HS_WIDE_OFF");
     r.wide_min_m = env_int("HS_WIDE_MIN_M");
+    r.tune = env_int("HS_TUNE");
+    r.mid_off = env_int("HS_MID_OFF");
+    r.mid_min_m = env_int("HS_MID_MIN_M");
+    r.mid_nj = env_int("HS_MID_NJ");
     r.prefill_wg_per_cu = env_int("HS_PREFILL_WG_PER_CU");
     return r;
   }();
@@ -115,6 +126,8 @@ struct Plan {
   bool stream = false;  // streaming decode kernel (fast path)
   bool decode = true;
   bool wide = false;    // 256x256-tile prefill kernel
+  bool mid = false;     // LDS-DMA streaming kernel, 32-row MFMA blocks
+  int BMI = 1, NJ = 1;
   int MT = 1, S = 1, BM = 256, NB = 1;
   int T = 0, TM = 1, G = 0;
   int64_t U = 0;
@@ -130,10 +143,25 @@ int stream_nb(int M) { return M <= 16 ? 8 : (M <= 32 ? 4 : 2); }
 
 // `fast`: the streaming kernel can run this problem (see stream_ok); `wide`:
 // the 256x256-tile prefill kernel can (see wide_ok).
-Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast, bool wide) {
+Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast, bool wide, bool mid) {
   Plan p;
   const int cus = device_cus();
   const Tuning& tn = tuning();
+  if (mid && !tn.mid_off && M >= (tn.mid_min_m > 0 ? tn.mid_min_m : 17) && M <= 64) {
+    p.mid = true;
+    p.BMI = M <= 32 ? 1 : 2;
+    // Wide outputs: 256 weight rows per tile; narrow ones 128, so that
+    // enough tiles exist and fewer of them are split across workgroups.
+    p.NJ = tn.mid_nj == 1 || tn.mid_nj == 2 ? tn.mid_nj : (N >= 16384 ? 2 : 1);
+    p.T = static_cast<int>(cdiv(N, 128 * p.NJ));
+    p.G = K / 64;
+    p.U = static_cast<int64_t>(p.T) * p.G;
+    p.P = static_cast<int>(p.U < cus ? p.U : cus);
+    p.slot_floats = mid_slot_floats(p.BMI, p.NJ);
+    p.counter_bytes = kCounterBytes;
+    p.ws_bytes = p.counter_bytes + static_cast<int64_t>(p.P) * 2 * p.slot_floats * 4;
+    return p;
+  }
   if (M <= kDecodeMaxM && fast && !tn.st_off) {
     p.stream = true;
     p.MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
@@ -232,8 +260,8 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
     }
   }
   const int nb = tn.st_nb > 0 ? tn.st_nb : stream_nb(a.M);
-  const Plan p =
-      make_plan(wt, a.M, a.N, a.K, decode_kfull(a.K, a.xvec, a.wvec), stream_ok(a, wt, nb), wide_ok(a, wt));
+  const Plan p = make_plan(wt, a.M, a.N, a.K, decode_kfull(a.K, a.xvec, a.wvec), stream_ok(a, wt, nb),
+                           wide_ok(a, wt), mid_ok(a, wt));
   if (p.T > kMaxTiles) return HS_EUNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < p.ws_bytes) return HS_EWORKSPACE;
   a.G = p.G;
@@ -244,7 +272,8 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   a.P = p.P;
   a.counters = reinterpret_cast<int*>(workspace);
   a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.counter_bytes);
-  hipError_t e = p.stream   ? launch_stream(wt, a, p.MT, p.S, stream)
+  hipError_t e = p.mid      ? launch_mid(wt, a, p.BMI, p.NJ, stream)
+                 : p.stream ? launch_stream(wt, a, p.MT, p.S, stream)
                  : p.decode ? launch_decode(wt, a, p.MT, p.S, stream)
                  : p.wide   ? launch_wide(wt, a, stream)
                             : launch_prefill(wt, a, p.BM, stream);
@@ -276,10 +305,11 @@ int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
   int64_t best = 0;
   for (int kfull = 0; kfull < 2; ++kfull)
     for (int fast = 0; fast < 2; ++fast)
-      for (int wide = 0; wide < 2; ++wide) {
-        const int64_t b = hsq::make_plan(kind, M, N, K, kfull != 0, fast != 0, wide != 0).ws_bytes;
-        best = b > best ? b : best;
-      }
+      for (int wide = 0; wide < 2; ++wide)
+        for (int mid = 0; mid < 2; ++mid) {
+          const int64_t b = hsq::make_plan(kind, M, N, K, kfull != 0, fast != 0, wide != 0, mid != 0).ws_bytes;
+          best = b > best ? b : best;
+        }
   return best;
 }
 
@@ -310,6 +340,7 @@ int hs_int4_gemm(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_p
   a.N = N;
   a.K = K;
   a.wvec = hsq::aligned16(packed) && (ld_packed % 4 == 0);
+  a.tune = hsq::tuning().tune;
   return hsq::run_gemm(hsq::W_INT4, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
@@ -339,6 +370,7 @@ int hs_fp8_gemm(const void* x, int64_t ldx, const uint8_t* data, int64_t ld_data
   a.N = N;
   a.K = K;
   a.wvec = hsq::aligned16(data) && (ld_data % 16 == 0);
+  a.tune = hsq::tuning().tune;
   return hsq::run_gemm(hsq::W_FP8, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 

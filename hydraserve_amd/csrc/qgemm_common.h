@@ -53,6 +53,7 @@ struct GemmArgs {
   float* partials;    // [P][2][slot] fp32 partial tiles
   int xvec;           // X base and row stride allow 16-byte loads
   int wvec;           // W base and row stride allow 16-byte loads
+  int tune;           // kernel-specific experiment bits (0 = defaults)
 };
 
 template <int SDT>
@@ -118,15 +119,9 @@ __device__ __forceinline__ int partial_slot(int p, int t, int G, int64_t U, int 
 // Partial tiles cross workgroups that may run on different XCDs, whose L2s are
 // not coherent with each other.  Instead of agent-scope release/acquire
 // fences (which write back and invalidate the whole L2), partials are written
-// with write-through agent-scope stores and read with agent-scope loads, and
+// and read with the cache policy of agent-scope atomics (sc1: write-through on
+// stores, coherent on loads; see store_partial4 / load_partial4 below), and
 // the arrival counter is an agent-scope atomic.
-__device__ __forceinline__ void store_partial(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float load_partial(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Count this workgroup's arrival at tile t once every thread's partial stores
 // are acknowledged; true in every thread of the workgroup that arrived last.
@@ -139,6 +134,25 @@ __device__ __forceinline__ bool arrive_last(int* counters, int t, int contributo
   }
   __syncthreads();
   return *lds_flag != 0;
+}
+
+// Partial tiles as 16-byte buffer accesses carrying the cache policy the
+// compiler gives agent-scope atomic loads and stores (sc1): as coherent
+// across XCDs as 4-byte atomics, but not ordered one after another, so a
+// settle keeps all of its loads in flight at once (atomic loads are issued
+// one round trip at a time, ~1 us each).
+constexpr int kAgentCoherent = 16;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(float* partials) {
+  return __builtin_amdgcn_make_buffer_rsrc(partials, static_cast<short>(0), 0x7FFFFFFF, 0x00020000);
+}
+
+__device__ __forceinline__ void store_partial4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, byte_off, 0, kAgentCoherent);
+}
+
+__device__ __forceinline__ f32x4_t load_partial4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kAgentCoherent));
 }
 
 __device__ __forceinline__ void reset_counter(int* counters, int t) {

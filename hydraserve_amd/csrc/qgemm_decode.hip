@@ -300,15 +300,15 @@ struct Decode {
   }
 
   static constexpr int SLOT = 4 * S * MT * 4 * 64;  // floats per partial slot
-  // Partial layout: element e of block (wave, s, i) of a lane at
-  // (((wave*S + s)*MT + i)*4 + e)*64 + lane, so each store or load
-  // instruction covers 256 contiguous bytes.
-  static __device__ __forceinline__ int64_t part_off(int wave, int s, int i, int lane) {
-    return (static_cast<int64_t>(wave * S + s) * MT + i) * 256 + lane;
+  // Partial layout (bytes in a slot): the f32x4 accumulator of block
+  // b = (wave*S + s)*MT + i of a lane at (b*64 + lane)*16, so every 16-byte
+  // store or load covers 1 KB.
+  static __device__ __forceinline__ uint32_t part_off(int wave, int s, int i, int lane) {
+    return static_cast<uint32_t>((((wave * S + s) * MT + i) * 64 + lane) * 16);
   }
 
-  static __device__ __forceinline__ float* slot_ptr(const GemmArgs& a, int p, int slot) {
-    return a.partials + (static_cast<int64_t>(p) * 2 + slot) * SLOT;
+  static __device__ __forceinline__ uint32_t slot_off(int p, int slot) {
+    return static_cast<uint32_t>((p * 2 + slot) * SLOT * 4);
   }
 
   static __device__ __forceinline__ void finish_tile(const GemmArgs& a, Smem& sm, f32x4_t (&acc)[S][MT], int t,
@@ -320,13 +320,12 @@ struct Decode {
       return;
     }
     const int pf = unit_owner(ts, a.U, a.P), pl = unit_owner(te - 1, a.U, a.P);
-    float* mine = slot_ptr(a, p, partial_slot(p, t, a.G, a.U, a.P));
+    const auto pr = partial_rsrc(a.partials);
+    const uint32_t mine = slot_off(p, partial_slot(p, t, a.G, a.U, a.P));
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) store_partial(mine + part_off(wave, s, i, lane) + e * 64, acc[s][i][e]);
+      for (int i = 0; i < MT; ++i) store_partial4(pr, mine + part_off(wave, s, i, lane), acc[s][i]);
     if (!arrive_last(a.counters, t, pl - pf + 1, &sm.flag)) return;
     // Sum every contributor's slot (our own included) in workgroup order.
 #pragma unroll
@@ -334,13 +333,11 @@ struct Decode {
 #pragma unroll
       for (int i = 0; i < MT; ++i) acc[s][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     for (int q = pf; q <= pl; ++q) {
-      const float* src = slot_ptr(a, q, partial_slot(q, t, a.G, a.U, a.P));
+      const uint32_t base = slot_off(q, partial_slot(q, t, a.G, a.U, a.P));
 #pragma unroll
       for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[s][i][e] += load_partial(src + part_off(wave, s, i, lane) + e * 64);
+        for (int i = 0; i < MT; ++i) acc[s][i] += load_partial4(pr, base + part_off(wave, s, i, lane));
     }
     store_tile(a, acc, t, wave, l16, h);
     reset_counter(a.counters, t);

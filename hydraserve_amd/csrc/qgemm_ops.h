@@ -84,18 +84,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64
 }
 
 // soff is uniform by construction; readfirstlane states it, so the compiler
-// never wraps the load in a per-lane loop.
-template <typename V>
+// never wraps the load in a per-lane loop.  AUX is the cache-policy operand
+// (kNonTemporal: data read once, streamed past the caches it would evict).
+constexpr int kNonTemporal = 2;
+
+template <typename V, int AUX = 0>
 __device__ __forceinline__ V bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff_in) {
   const uint32_t soff = __builtin_amdgcn_readfirstlane(soff_in);
   if constexpr (sizeof(V) == 16) {
-    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
   } else if constexpr (sizeof(V) == 8) {
-    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, AUX));
   } else if constexpr (sizeof(V) == 4) {
-    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, AUX));
   } else {
-    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, AUX));
   }
 }
 

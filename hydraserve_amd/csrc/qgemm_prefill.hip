@@ -215,15 +215,15 @@ struct Prefill {
   }
 
   static constexpr int SLOT = 4 * MI * 2 * 16 * 64;
-  // Partial layout: element e of block (i, j) of a lane at
-  // ((((wave*MI + i)*2 + j)*16 + e)*64 + lane, so each store or load
-  // instruction covers 256 contiguous bytes.
-  static __device__ __forceinline__ int64_t part_off(int wave, int i, int j, int lane) {
-    return (static_cast<int64_t>(wave * MI + i) * 2 + j) * 1024 + lane;
+  // Partial layout (bytes in a slot): 16-byte chunk v (elements 4v..4v+3)
+  // of accumulator block b = (wave*MI + i)*2 + j of a lane at
+  // ((b*4 + v)*64 + lane)*16, so every 16-byte store or load covers 1 KB.
+  static __device__ __forceinline__ uint32_t part_off(int b, int v, int lane) {
+    return static_cast<uint32_t>(((b * 4 + v) * 64 + lane) * 16);
   }
 
-  static __device__ __forceinline__ float* slot_ptr(const GemmArgs& a, int p, int slot) {
-    return a.partials + (static_cast<int64_t>(p) * 2 + slot) * SLOT;
+  static __device__ __forceinline__ uint32_t slot_off(int p, int slot) {
+    return static_cast<uint32_t>((p * 2 + slot) * SLOT * 4);
   }
 
   static __device__ __forceinline__ void finish_tile(const GemmArgs& a, Smem& sm, f32x16_t (&acc)[MI][2], int t,
@@ -235,14 +235,16 @@ struct Prefill {
       return;
     }
     const int pf = unit_owner(ts, a.U, a.P), pl = unit_owner(te - 1, a.U, a.P);
-    float* mine = slot_ptr(a, p, partial_slot(p, t, a.G, a.U, a.P));
+    const auto pr = partial_rsrc(a.partials);
+    const uint32_t mine = slot_off(p, partial_slot(p, t, a.G, a.U, a.P));
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        float* dst = mine + part_off(wave, i, j, lane);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) store_partial(dst + e * 64, acc[i][j][e]);
+        for (int v = 0; v < 4; ++v)
+          store_partial4(pr, mine + part_off((wave * MI + i) * 2 + j, v, lane),
+                         f32x4_t{acc[i][j][4 * v], acc[i][j][4 * v + 1], acc[i][j][4 * v + 2], acc[i][j][4 * v + 3]});
         __builtin_amdgcn_sched_barrier(0);
       }
     if (!arrive_last(a.counters, t, pl - pf + 1, &sm.flag)) return;
@@ -250,16 +252,17 @@ struct Prefill {
 #pragma unroll
     for (int i = 0; i < MI; ++i) acc[i][0] = acc[i][1] = f32x16_t{};
     for (int q = pf; q <= pl; ++q) {
-      const float* src = slot_ptr(a, q, partial_slot(q, t, a.G, a.U, a.P));
+      const uint32_t base = slot_off(q, partial_slot(q, t, a.G, a.U, a.P));
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const float* sp = src + part_off(wave, i, j, lane);
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) acc[i][j][e] += load_partial(sp + e * 64);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+          for (int v = 0; v < 4; ++v) {
+            const f32x4_t x = load_partial4(pr, base + part_off((wave * MI + i) * 2 + j, v, lane));
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[i][j][4 * v + c] += x[c];
+          }
     }
     store_tile(a, acc, t, wave, l32, h);
     reset_counter(a.counters, t);

@@ -387,14 +387,14 @@ struct Stream {
   }
 
   static constexpr int SLOT = 4 * S * MT * 4 * 64;
-  static __device__ __forceinline__ float* slot_ptr(const GemmArgs& a, int p, int slot) {
-    return a.partials + (static_cast<int64_t>(p) * 2 + slot) * SLOT;
+  static __device__ __forceinline__ uint32_t slot_off(int p, int slot) {
+    return static_cast<uint32_t>((p * 2 + slot) * SLOT * 4);
   }
-  // Element e of block (wave, s, i) of a lane sits at
-  // (((wave*S + s)*MT + i)*4 + e)*64 + lane: each store or load instruction
-  // covers 256 contiguous bytes.
-  static __device__ __forceinline__ int part_off(int wave, int s, int i, int lane) {
-    return ((wave * S + s) * MT + i) * 256 + lane;
+  // The f32x4 accumulator of block (wave, s, i) of a lane sits at byte
+  // (((wave*S + s)*MT + i)*64 + lane)*16 of the slot: every 16-byte store or
+  // load covers 1 KB.
+  static __device__ __forceinline__ uint32_t part_off(int wave, int s, int i, int lane) {
+    return static_cast<uint32_t>((((wave * S + s) * MT + i) * 64 + lane) * 16);
   }
 
   // End of tile t inside this workgroup's range.  A tile the range covers
@@ -409,13 +409,12 @@ struct Stream {
       store_tile(a, acc, t, wave, l16, h);
       return false;
     }
-    float* mine = slot_ptr(a, p, partial_slot(p, t, a.G, a.U, a.P));
+    const auto pr = partial_rsrc(a.partials);
+    const uint32_t mine = slot_off(p, partial_slot(p, t, a.G, a.U, a.P));
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) store_partial(mine + part_off(wave, s, i, lane) + e * 64, acc[s][i][e]);
+      for (int i = 0; i < MT; ++i) store_partial4(pr, mine + part_off(wave, s, i, lane), acc[s][i]);
     return true;
   }
 
@@ -423,7 +422,7 @@ struct Stream {
   // done: one drain for the partial stores, one arrival round for both
   // tiles; the last contributor of a tile sums every partial in workgroup
   // order (deterministic), stores bf16 and resets the counter.  Partial loads
-  // are issued four contributors at a time before any is summed.
+  // are 16-byte coherent loads that stay in flight together.
   static __device__ __forceinline__ void settle(const GemmArgs& a, int* flag, int t0, int t1, int tid) {
     const int wave = tid >> 6, lane = tid & 63, l16 = lane & 15, h = lane >> 4;
     int pf[2], pl[2];
@@ -457,29 +456,13 @@ struct Stream {
       for (int s = 0; s < S; ++s)
 #pragma unroll
         for (int i = 0; i < MT; ++i) acc[s][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      for (int q0 = pf[k]; q0 <= pl[k]; q0 += 4) {
-        float v[4][S][MT][4];
+      const auto pr = partial_rsrc(a.partials);
+      for (int q = pf[k]; q <= pl[k]; ++q) {
+        const uint32_t base = slot_off(q, partial_slot(q, t, a.G, a.U, a.P));
 #pragma unroll
-        for (int dq = 0; dq < 4; ++dq) {
-          const int q = q0 + dq <= pl[k] ? q0 + dq : pl[k];
-          const float* src = slot_ptr(a, q, partial_slot(q, t, a.G, a.U, a.P));
+        for (int s = 0; s < S; ++s)
 #pragma unroll
-          for (int s = 0; s < S; ++s)
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[dq][s][i][e] = load_partial(src + part_off(wave, s, i, lane) + e * 64);
-        }
-#pragma unroll
-        for (int dq = 0; dq < 4; ++dq) {
-          if (q0 + dq > pl[k]) break;
-#pragma unroll
-          for (int s = 0; s < S; ++s)
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) acc[s][i][e] += v[dq][s][i][e];
-        }
+          for (int i = 0; i < MT; ++i) acc[s][i] += load_partial4(pr, base + part_off(wave, s, i, lane));
       }
       store_tile(a, acc, t, wave, l16, h);
       if (tid == 0) __hip_atomic_store(&a.counters[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

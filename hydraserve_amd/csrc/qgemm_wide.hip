@@ -62,8 +62,10 @@ struct Wide {
   static constexpr int SLOT = 4 * MI * 2 * 16 * 64;  // floats of one partial tile
 
   // X ring: tile row r (128 bytes) holds its 16-byte K segment g at slot
-  // g ^ (r & 7), so the 16-byte A-fragment reads of 8 consecutive rows hit
-  // 8 distinct bank groups.
+  // g ^ ((r >> 1) & 7).  A 16-byte LDS read serves 16 lanes per pass; with
+  // rows 128 bytes apart, rows r and r+1 fall in opposite halves of the 64
+  // banks and the XOR gives the 8 rows of each parity 8 distinct 16-byte bank
+  // groups, so the A-fragment reads of 16 consecutive rows are conflict-free.
   struct Smem {
     __attribute__((aligned(1024))) uint8_t xs[3][XB];
     int flag;
@@ -96,13 +98,15 @@ struct Wide {
   static __device__ __forceinline__ void offsets(const GemmArgs& a, Offs& o, int tm, int tn, int wave, int l32,
                                                  int h, int tid) {
     // Load q of wave w fills LDS rows 8(4q + w) .. +8 (1 KB, lane l at byte
-    // 16 l): row 8(4q + w) + l/8, slot l%8, i.e. K segment (l%8) ^ (l/8).
+    // 16 l): tile row r = 8(4q + w) + l/8, slot l%8, i.e. K segment
+    // (l%8) ^ ((r >> 1) & 7).
     const int lane = tid & 63;
 #pragma unroll
     for (int q = 0; q < XR; ++q) {
-      int row = tm * BM + 8 * (4 * q + wave) + (lane >> 3);
+      const int r = 8 * (4 * q + wave) + (lane >> 3);
+      int row = tm * BM + r;
       row = row < a.M ? row : a.M - 1;
-      const int seg = (lane & 7) ^ (lane >> 3);
+      const int seg = (lane & 7) ^ ((r >> 1) & 7);
       o.x[q] = static_cast<uint32_t>((row * a.ldx + seg * 8) * 2);
     }
     constexpr int SES = SDT == SCALE_F32 ? 4 : 2;
@@ -219,7 +223,7 @@ struct Wide {
   }
 
   // A fragment of row block i, step t: row 32i + l32, K segment 4h + t.
-  // aoff[t] = l32*128 + ((4h + t) ^ (l32 & 7))*16.
+  // aoff[t] = l32*128 + ((4h + t) ^ ((l32 >> 1) & 7))*16.
   static __device__ __forceinline__ bf16x8_t read_a(const Smem& sm, int buf, uint32_t aoff, int i) {
     return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(&sm.xs[0][0] + buf + aoff + 4096 * i));
   }
@@ -267,6 +271,9 @@ struct Wide {
       for (int i = 0; i < MI; ++i) A[i] = An[i];
       B[0] = Bn[0];
       B[1] = Bn[1];
+      // Keep the next step's MFMAs (which consume the reads just issued)
+      // out of this step, so LDS latency hides behind this step's MFMAs.
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -289,15 +296,15 @@ struct Wide {
     }
   }
 
-  // Partial layout: element e of block (i, j) of a lane at
-  // ((((wave*MI + i)*2 + j)*16 + e)*64 + lane: every store or load
-  // instruction covers 256 contiguous bytes.
-  static __device__ __forceinline__ int64_t part_off(int wave, int i, int j, int lane) {
-    return (static_cast<int64_t>(wave * MI + i) * 2 + j) * 1024 + lane;
+  // Partial layout (bytes in a slot): 16-byte chunk v (elements 4v..4v+3)
+  // of accumulator block b = (wave*MI + i)*2 + j of a lane at
+  // ((b*4 + v)*64 + lane)*16, so every 16-byte store or load covers 1 KB.
+  static __device__ __forceinline__ uint32_t part_off(int b, int v, int lane) {
+    return static_cast<uint32_t>(((b * 4 + v) * 64 + lane) * 16);
   }
 
-  static __device__ __forceinline__ float* slot_ptr(const GemmArgs& a, int v, int slot) {
-    return a.partials + (static_cast<int64_t>(v) * 2 + slot) * SLOT;
+  static __device__ __forceinline__ uint32_t slot_off(int v, int slot) {
+    return static_cast<uint32_t>((v * 2 + slot) * SLOT * 4);
   }
 
   static __device__ __forceinline__ void finish_tile(const GemmArgs& a, Smem& sm, f32x16_t (&acc)[MI][2], int t,
@@ -309,36 +316,56 @@ struct Wide {
       return;
     }
     const int pf = unit_owner(ts, a.U, a.P), pl = unit_owner(te - 1, a.U, a.P);
-    float* mine = slot_ptr(a, v, partial_slot(v, t, a.G, a.U, a.P));
+    const auto pr = partial_rsrc(a.partials);
+    const uint32_t mine = slot_off(v, partial_slot(v, t, a.G, a.U, a.P));
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        float* dst = mine + part_off(wave, i, j, lane);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) store_partial(dst + e * 64, acc[i][j][e]);
+        for (int c4 = 0; c4 < 4; ++c4)
+          store_partial4(pr, mine + part_off((wave * MI + i) * 2 + j, c4, lane),
+                         f32x4_t{acc[i][j][4 * c4], acc[i][j][4 * c4 + 1], acc[i][j][4 * c4 + 2], acc[i][j][4 * c4 + 3]});
         __builtin_amdgcn_sched_barrier(0);
       }
     if (!arrive_last(a.counters, t, pl - pf + 1, &sm.flag)) return;
-    // Sum every contributor's slot (ours included) in workgroup order, one
-    // 32x32 block at a time, and store it.
+    // Sum every contributor's slot (ours included) in workgroup order, two
+    // row blocks at a time: all 16 of a contributor's 16-byte loads for them
+    // are in flight before any is summed.
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int i0 = 0; i0 < MI; i0 += 2) {
+      f32x16_t sum[2][2] = {};
+      for (int q = pf; q <= pl; ++q) {
+        const uint32_t base = slot_off(q, partial_slot(q, t, a.G, a.U, a.P));
+        f32x4_t x[2][2][4];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4)
+              x[ii][j][c4] = load_partial4(pr, base + part_off((wave * MI + i0 + ii) * 2 + j, c4, lane));
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+              for (int c = 0; c < 4; ++c) sum[ii][j][4 * c4 + c] += x[ii][j][c4][c];
+      }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        f32x16_t sum = {};
-        for (int q = pf; q <= pl; ++q) {
-          const float* sp = slot_ptr(a, q, partial_slot(q, t, a.G, a.U, a.P)) + part_off(wave, i, j, lane);
-#pragma unroll
-          for (int e = 0; e < 16; ++e) sum[e] += load_partial(sp + e * 64);
-        }
         const int n = tn * BN + wave * 64 + 32 * j + l32;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = tm * BM + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-          if (m < a.M && n < a.N) a.y[m * a.ldy + n] = to_bf16_bits(sum[e]);
-        }
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int m = tm * BM + 32 * (i0 + ii) + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (m < a.M && n < a.N) a.y[m * a.ldy + n] = to_bf16_bits(sum[ii][j][e]);
+          }
       }
+    }
     reset_counter(a.counters, t);
   }
 };
@@ -354,7 +381,7 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
   const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
   const int p = blockIdx.x;
   // Workgroups of one XCD (p % 8) take one contiguous run of units.
-  const int v = (a.P % 8 == 0) ? (p % 8) * (a.P / 8) + p / 8 : p;
+  const int v = (a.P % 8 == 0 && !(a.tune & 1)) ? (p % 8) * (a.P / 8) + p / 8 : p;
   const int64_t u0 = unit_begin(v, a.U, a.P), u1 = unit_begin(v + 1, a.U, a.P);
   // Byte extents of the buffers (wide_ok keeps them below 2^32).
   typename W::Rsrc rs;
@@ -372,7 +399,7 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
 
   uint32_t aoff[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) aoff[t] = l32 * 128 + (((4 * h + t) ^ (l32 & 7)) * 16);
+  for (int t = 0; t < 4; ++t) aoff[t] = l32 * 128 + (((4 * h + t) ^ ((l32 >> 1) & 7)) * 16);
 
   int64_t u = u0;
   while (u < u1) {
