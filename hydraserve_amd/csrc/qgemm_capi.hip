@@ -23,8 +23,8 @@ bool stream_ok(const GemmArgs& a, int wt, int NB);
 bool decode_kfull(int K, int xvec, int wvec);
 int prefill_slot_floats(int BM);
 hipError_t launch_wide(int wt, const GemmArgs& a, hipStream_t stream);
-hipError_t launch_mid(int wt, const GemmArgs& a, int bmi, int nj, hipStream_t stream);
-int mid_slot_floats(int bmi, int nj);
+hipError_t launch_mid(int wt, const GemmArgs& a, int bmi, int nj, int nw, hipStream_t stream);
+int mid_slot_floats(int bmi, int nj, int nw);
 bool mid_ok(const GemmArgs& a, int wt);
 int wide_slot_floats();
 bool wide_ok(const GemmArgs& a, int wt);
@@ -69,6 +69,7 @@ struct Tuning {
   int mid_off = 0;         // 1: never use the LDS-DMA streaming kernel for 17..64 rows
   int mid_min_m = 0;       // smallest M for it (0 = 17)
   int mid_nj = 0;          // its 32-column blocks per wave (0 = heuristic)
+  int mid_nw = 0;          // its wavefronts per workgroup (0 = heuristic)
   int prefill_wg_per_cu = 0;
 };
 
@@ -102,6 +103,7 @@ const Tuning& tuning() {
     r.mid_off = env_int("HS_MID_OFF");
     r.mid_min_m = env_int("HS_MID_MIN_M");
     r.mid_nj = env_int("HS_MID_NJ");
+    r.mid_nw = env_int("HS_MID_NW");
     r.prefill_wg_per_cu = env_int("HS_PREFILL_WG_PER_CU");
     return r;
   }();
@@ -127,7 +129,7 @@ struct Plan {
   bool decode = true;
   bool wide = false;    // 256x256-tile prefill kernel
   bool mid = false;     // LDS-DMA streaming kernel, 32-row MFMA blocks
-  int BMI = 1, NJ = 1;
+  int BMI = 1, NJ = 1, NW = 4;
   int MT = 1, S = 1, BM = 256, NB = 1;
   int T = 0, TM = 1, G = 0;
   int64_t U = 0;
@@ -153,11 +155,19 @@ Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast, bool wide, bo
     // Wide outputs: 256 weight rows per tile; narrow ones 128, so that
     // enough tiles exist and fewer of them are split across workgroups.
     p.NJ = tn.mid_nj == 1 || tn.mid_nj == 2 ? tn.mid_nj : (N >= 16384 ? 2 : 1);
-    p.T = static_cast<int>(cdiv(N, 128 * p.NJ));
+    // 8 waves of one column block each (two waves per SIMD, 33..64 rows)
+    // measured no faster than 4 waves of two: the SIMDs' VALU and MFMA work
+    // per unit is the same either way.
+    p.NW = tn.mid_nw == 4 || tn.mid_nw == 8 ? tn.mid_nw : 4;
+    if (p.NW == 8) {
+      if (p.BMI != 2) p.NW = 4;
+      else p.NJ = 1;
+    }
+    p.T = static_cast<int>(cdiv(N, 32 * p.NJ * p.NW));
     p.G = K / 64;
     p.U = static_cast<int64_t>(p.T) * p.G;
     p.P = static_cast<int>(p.U < cus ? p.U : cus);
-    p.slot_floats = mid_slot_floats(p.BMI, p.NJ);
+    p.slot_floats = mid_slot_floats(p.BMI, p.NJ, p.NW);
     p.counter_bytes = kCounterBytes;
     p.ws_bytes = p.counter_bytes + static_cast<int64_t>(p.P) * 2 * p.slot_floats * 4;
     return p;
@@ -272,7 +282,7 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   a.P = p.P;
   a.counters = reinterpret_cast<int*>(workspace);
   a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.counter_bytes);
-  hipError_t e = p.mid      ? launch_mid(wt, a, p.BMI, p.NJ, stream)
+  hipError_t e = p.mid      ? launch_mid(wt, a, p.BMI, p.NJ, p.NW, stream)
                  : p.stream ? launch_stream(wt, a, p.MT, p.S, stream)
                  : p.decode ? launch_decode(wt, a, p.MT, p.S, stream)
                  : p.wide   ? launch_wide(wt, a, stream)

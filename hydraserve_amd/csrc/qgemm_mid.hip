@@ -7,9 +7,12 @@
 // the weight stream is still the roofline but every weight feeds 32-64
 // output rows.
 //
-//   * A workgroup (4 wavefronts) owns a BM x BN output tile, BM = 32*BMI rows
-//     (all of M), BN = 128*NJ weight rows; wave w owns weight rows
-//     [32*NJ*w, +32*NJ): BMI x NJ blocks of 32x32 fp32 accumulators.
+//   * A workgroup (NW = 4 or 8 wavefronts) owns a BM x BN output tile,
+//     BM = 32*BMI rows (all of M), BN = 32*NJ*NW weight rows; wave w owns
+//     weight rows [32*NJ*w, +32*NJ): BMI x NJ blocks of 32x32 fp32
+//     accumulators.  With 8 waves each holds half the registers and two
+//     share every SIMD, so one wave's LDS and VALU latency hides behind the
+//     other's work.
 //   * K advances 64 per unit; units are scheduled stream-K over a persistent
 //     grid.  Everything a unit needs -- the X tile [BM x 64] (shared by the
 //     four waves), each wave's packed weights, scales and (INT4) zero-point
@@ -40,27 +43,28 @@
 
 namespace hsq {
 
-constexpr int MID_THREADS = 256;
 constexpr int MID_D = 6;  // ring depth (units)
 
-template <int WT, int SDT, int BMI, int NJ>
+template <int WT, int SDT, int BMI, int NJ, int NW>
 struct Mid {
+  static_assert((4 * BMI) % NW == 0, "every wave issues the same number of X loads");
   static constexpr int D = MID_D;
+  static constexpr int THREADS = 64 * NW;
   static constexpr int BM = 32 * BMI;
-  static constexpr int BN = 128 * NJ;
+  static constexpr int BN = 32 * NJ * NW;
   static constexpr int RB = WT == W_INT4 ? 32 : 64;  // weight bytes per row per unit
   static constexpr int RW = WT == W_INT4 ? 1 : 2;    // 16-byte reads per row per unit
   static constexpr int XB = BM * 128;
   static constexpr int WBW = 32 * NJ * RB;  // weight bytes per wave per unit
   static constexpr int SBW = 256;           // scale bytes per wave
   static constexpr int ZBW = WT == W_INT4 ? 256 : 0;
-  static constexpr int SLOTB = XB + 4 * (WBW + SBW + ZBW);
+  static constexpr int SLOTB = XB + NW * (WBW + SBW + ZBW);
   // LDS-DMA loads per wave per unit: X, weights, scales, zero points.
-  static constexpr int LX = BMI;
+  static constexpr int LX = 4 * BMI / NW;
   static constexpr int LW = WBW / 1024;
   static constexpr int L = LX + LW + 1 + (WT == W_INT4 ? 1 : 0);
   static constexpr int SES = SDT == SCALE_F32 ? 4 : 2;
-  static constexpr int SLOT = 4 * BMI * NJ * 1024;  // floats of one partial tile
+  static constexpr int SLOT = NW * BMI * NJ * 1024;  // floats of one partial tile
 
   struct Smem {
     __attribute__((aligned(1024))) uint8_t ring[D][SLOTB];
@@ -90,11 +94,11 @@ struct Mid {
   };
 
   static __device__ __forceinline__ void sources(const GemmArgs& a, Src& s, int wave, int lane) {
-    // X load q of wave w fills tile rows 8(4q + w) .. +8: row r = 8(4q + w) + lane/8,
+    // X load q of wave w fills tile rows 8(NW*q + w) .. +8: row r = 8(NW*q + w) + lane/8,
     // slot lane%8 = K segment (lane%8) ^ ((r >> 1) & 7).  Rows past M repeat M-1.
 #pragma unroll
     for (int q = 0; q < LX; ++q) {
-      const int r = 8 * (4 * q + wave) + (lane >> 3);
+      const int r = 8 * (NW * q + wave) + (lane >> 3);
       const int row = r < a.M ? r : a.M - 1;
       const int seg = (lane & 7) ^ ((r >> 1) & 7);
       s.x[q] = static_cast<uint32_t>((row * a.ldx + seg * 8) * 2);
@@ -123,7 +127,7 @@ struct Mid {
     const uint32_t kx = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c) * 128u);
 #pragma unroll
     for (int q = 0; q < LX; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.x, base + 1024 * (4 * q + wave), 16, s.x[q], kx, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.x, base + 1024 * (NW * q + wave), 16, s.x[q], kx, 0, 0);
     const int row0 = t * BN + wave * 32 * NJ;  // first weight row of the wave
     uint8_t* wbase = base + woff(wave);
 #pragma unroll
@@ -311,9 +315,9 @@ struct Mid {
 
 // a.G = 64-wide K units per tile, a.T = tiles (BN weight rows each; BM >= M),
 // a.U = T * G, a.P = workgroups.
-template <int WT, int SDT, int BMI, int NJ>
-__global__ __launch_bounds__(MID_THREADS, 1) void qgemm_mid_kernel(GemmArgs a) {
-  using K = Mid<WT, SDT, BMI, NJ>;
+template <int WT, int SDT, int BMI, int NJ, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void qgemm_mid_kernel(GemmArgs a) {
+  using K = Mid<WT, SDT, BMI, NJ, NW>;
   constexpr int D = K::D;
   __shared__ typename K::Smem sm;
   const int tid = threadIdx.x;
@@ -456,13 +460,13 @@ __global__ __launch_bounds__(MID_THREADS, 1) void qgemm_mid_kernel(GemmArgs a) {
   __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
-template <int WT, int SDT, int BMI, int NJ>
+template <int WT, int SDT, int BMI, int NJ, int NW>
 static hipError_t launch_mid_t(const GemmArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((qgemm_mid_kernel<WT, SDT, BMI, NJ>), dim3(a.P), dim3(MID_THREADS), 0, stream, a);
+  hipLaunchKernelGGL((qgemm_mid_kernel<WT, SDT, BMI, NJ, NW>), dim3(a.P), dim3(64 * NW), 0, stream, a);
   return hipGetLastError();
 }
 
-int mid_slot_floats(int bmi, int nj) { return 4 * bmi * nj * 1024; }
+int mid_slot_floats(int bmi, int nj, int nw) { return nw * bmi * nj * 1024; }
 
 // K a multiple of 128, 16-byte aligned rows, M <= 64, every buffer byte
 // offset below 2^31.
@@ -477,23 +481,27 @@ bool mid_ok(const GemmArgs& a, int wt) {
 }
 
 template <int WT, int SDT>
-static hipError_t launch_mid_s(const GemmArgs& a, int bmi, int nj, hipStream_t stream) {
-  if (bmi == 1 && nj == 1) return launch_mid_t<WT, SDT, 1, 1>(a, stream);
-  if (bmi == 1 && nj == 2) return launch_mid_t<WT, SDT, 1, 2>(a, stream);
-  if (bmi == 2 && nj == 1) return launch_mid_t<WT, SDT, 2, 1>(a, stream);
-  if (bmi == 2 && nj == 2) return launch_mid_t<WT, SDT, 2, 2>(a, stream);
+static hipError_t launch_mid_s(const GemmArgs& a, int bmi, int nj, int nw, hipStream_t stream) {
+  if (nw == 8) {
+    if (bmi == 2 && nj == 1) return launch_mid_t<WT, SDT, 2, 1, 8>(a, stream);
+    return hipErrorInvalidValue;
+  }
+  if (bmi == 1 && nj == 1) return launch_mid_t<WT, SDT, 1, 1, 4>(a, stream);
+  if (bmi == 1 && nj == 2) return launch_mid_t<WT, SDT, 1, 2, 4>(a, stream);
+  if (bmi == 2 && nj == 1) return launch_mid_t<WT, SDT, 2, 1, 4>(a, stream);
+  if (bmi == 2 && nj == 2) return launch_mid_t<WT, SDT, 2, 2, 4>(a, stream);
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_mid(int wt, const GemmArgs& a, int bmi, int nj, hipStream_t stream) {
+hipError_t launch_mid(int wt, const GemmArgs& a, int bmi, int nj, int nw, hipStream_t stream) {
   if (wt == W_INT4) {
-    if (a.sdt == SCALE_BF16) return launch_mid_s<W_INT4, SCALE_BF16>(a, bmi, nj, stream);
-    if (a.sdt == SCALE_F16) return launch_mid_s<W_INT4, SCALE_F16>(a, bmi, nj, stream);
-    return launch_mid_s<W_INT4, SCALE_F32>(a, bmi, nj, stream);
+    if (a.sdt == SCALE_BF16) return launch_mid_s<W_INT4, SCALE_BF16>(a, bmi, nj, nw, stream);
+    if (a.sdt == SCALE_F16) return launch_mid_s<W_INT4, SCALE_F16>(a, bmi, nj, nw, stream);
+    return launch_mid_s<W_INT4, SCALE_F32>(a, bmi, nj, nw, stream);
   }
-  if (a.sdt == SCALE_BF16) return launch_mid_s<W_FP8, SCALE_BF16>(a, bmi, nj, stream);
-  if (a.sdt == SCALE_F16) return launch_mid_s<W_FP8, SCALE_F16>(a, bmi, nj, stream);
-  return launch_mid_s<W_FP8, SCALE_F32>(a, bmi, nj, stream);
+  if (a.sdt == SCALE_BF16) return launch_mid_s<W_FP8, SCALE_BF16>(a, bmi, nj, nw, stream);
+  if (a.sdt == SCALE_F16) return launch_mid_s<W_FP8, SCALE_F16>(a, bmi, nj, nw, stream);
+  return launch_mid_s<W_FP8, SCALE_F32>(a, bmi, nj, nw, stream);
 }
 
 }  // namespace hsq
