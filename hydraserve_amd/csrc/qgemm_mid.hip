@@ -347,39 +347,43 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_mid_kernel(GemmArgs a) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) aoff[t] = l32 * 128 + (((4 * h + t) ^ ((l32 >> 1) & 7)) * 16);
 
-  // DMA cursor: the unit index (relative to u0) issued next, clamped to the
-  // range's last unit, and its tile/chunk.
-  int di = 0;
-  // Unit indices fit in 32 bits (the host caps the tile count).
-  const uint32_t ub = static_cast<uint32_t>(u0), G = static_cast<uint32_t>(a.G);
+  // DMA cursor: the next unit to load (tile dt, chunk dc), advanced without
+  // divisions and held at the range's last unit once the range is exhausted
+  // (those loads are harmless and never used).
+  const int t_first = static_cast<int>(u0 / a.G), c_first = static_cast<int>(u0 - static_cast<int64_t>(t_first) * a.G);
+  int dt = t_first, dc = c_first, di = 0;
   auto issue_next = [&](int slot_idx) __attribute__((always_inline)) {
-    const uint32_t ua = ub + static_cast<uint32_t>(di < total ? di : total - 1);
-    const int t = static_cast<int>(ua / G);
-    const int c = static_cast<int>(ua - static_cast<uint32_t>(t) * G);
-    K::issue(a, rs, src, sm, __builtin_amdgcn_readfirstlane(slot_idx * K::SLOTB), t, c, wave, lane);
-    ++di;
+    K::issue(a, rs, src, sm, __builtin_amdgcn_readfirstlane(slot_idx * K::SLOTB), dt, dc, wave, lane);
+    if (++di < total) {
+      if (++dc == a.G) {
+        dc = 0;
+        ++dt;
+      }
+    }
   };
-  auto tc_of = [&](int k, int& t, int& c) __attribute__((always_inline)) {
-    const uint32_t ua = ub + static_cast<uint32_t>(k < total ? k : total - 1);
-    t = static_cast<int>(ua / G);
-    c = static_cast<int>(ua - static_cast<uint32_t>(t) * G);
+  // Compute-side cursor of the unit after the current one (its raw data is
+  // read one unit ahead), same clamping.
+  int nt = t_first, nc = c_first, ni = 0;
+  auto advance_next = [&]() __attribute__((always_inline)) {
+    if (++ni < total) {
+      if (++nc == a.G) {
+        nc = 0;
+        ++nt;
+      }
+    }
   };
 
-  // Prologue: units 0 .. D-2 in flight; unit 0 landed, step 0 prepared.
+  // Prologue: unit 0 alone first (every workgroup's first loads then form a
+  // burst of one unit, not D-1: measured 6.5 us to the first unit otherwise),
+  // then units 1 .. D-2 in flight while unit 0 is computed.
+  issue_next(0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 #pragma unroll
-  for (int s = 0; s < D - 1; ++s) issue_next(s);
-  {
-    constexpr int later = (D - 2) * K::L;
-    __builtin_amdgcn_s_waitcnt((later & 15) | ((later >> 4) << 14) | 0x0F70);
-  }
+  for (int s = 1; s < D - 1; ++s) issue_next(s);
   __syncthreads();
   typename K::Raw r0, r1;
   bf16x8_t A[BMI], B[NJ];
-  {
-    int t, c;
-    tc_of(0, t, c);
-    K::read_raw(a, sm, r0, 0, t, c, wave, l32, h);
-  }
+  K::read_raw(a, sm, r0, 0, nt, nc, wave, l32, h);
 #pragma unroll
   for (int i = 0; i < BMI; ++i) A[i] = K::read_a(sm, 0, aoff[0], i);
 #pragma unroll
@@ -396,11 +400,8 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_mid_kernel(GemmArgs a) {
       __builtin_amdgcn_s_waitcnt((later & 15) | ((later >> 4) << 14) | 0x0F70);
     }
     issue_next((k + D - 1) % D);
-    {
-      int t, c;
-      tc_of(k + 1, t, c);
-      K::read_raw(a, sm, Rn, sn, t, c, wave, l32, h);
-    }
+    advance_next();
+    K::read_raw(a, sm, Rn, sn, nt, nc, wave, l32, h);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       if (t == 3) {
@@ -431,9 +432,8 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_mid_kernel(GemmArgs a) {
     ++k;
   };
 
+  int t = t_first, c = c_first;  // tile and chunk of unit k
   while (k < total) {
-    int t, c;
-    tc_of(k, t, c);
     const int n = (a.G - c) < (total - k) ? (a.G - c) : (total - k);
     f32x16_t acc[BMI][NJ];
 #pragma unroll
@@ -455,6 +455,8 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_mid_kernel(GemmArgs a) {
       unit(r1, r0, acc);
     }
     K::finish_tile(a, sm, acc, t, p, u0, u1, tid);
+    ++t;
+    c = 0;
   }
   // Drain the clamped prefetches before the workgroup exits.
   __builtin_amdgcn_s_waitcnt(0x0F70);
