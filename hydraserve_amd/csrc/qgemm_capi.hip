@@ -64,7 +64,7 @@ struct Tuning {
   int decode_wg_per_cu = 0;
   int prefill_bm = 0;
   int wide_off = 0;         // 1: never use the 256x256-tile prefill kernel
-  int wide_min_m = 0;      // smallest M for it (0 = 256)
+  int wide_min_m = 0;      // smallest M for it (0 = 129)
   int tune = 0;            // GemmArgs::tune experiment bits
   int mid_off = 0;         // 1: never use the LDS-DMA streaming kernel for 17..64 rows
   int mid_min_m = 0;       // smallest M for it (0 = 17)
@@ -149,18 +149,19 @@ Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast, bool wide, bo
   Plan p;
   const int cus = device_cus();
   const Tuning& tn = tuning();
-  if (mid && !tn.mid_off && M >= (tn.mid_min_m > 0 ? tn.mid_min_m : 17) && M <= 64) {
+  if (mid && !tn.mid_off && M >= (tn.mid_min_m > 0 ? tn.mid_min_m : 17) && M <= 128) {
     p.mid = true;
-    p.BMI = M <= 32 ? 1 : 2;
+    p.BMI = static_cast<int>(cdiv(M, 32));
     // Wide outputs: 256 weight rows per tile; narrow ones 128, so that
     // enough tiles exist and fewer of them are split across workgroups.
     p.NJ = tn.mid_nj == 1 || tn.mid_nj == 2 ? tn.mid_nj : (N >= 16384 ? 2 : 1);
+    if ((wt != W_INT4 && p.BMI > 2) || p.BMI > 3) p.NJ = 1;
     // 8 waves of one column block each (two waves per SIMD, 33..64 rows)
     // measured no faster than 4 waves of two: the SIMDs' VALU and MFMA work
     // per unit is the same either way.
     p.NW = tn.mid_nw == 4 || tn.mid_nw == 8 ? tn.mid_nw : 4;
     if (p.NW == 8) {
-      if (p.BMI != 2) p.NW = 4;
+      if (p.BMI != 2) p.NW = 4;  // the 8-wave layout is built for 2 row blocks only
       else p.NJ = 1;
     }
     p.T = static_cast<int>(cdiv(N, 32 * p.NJ * p.NW));
@@ -204,12 +205,10 @@ Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast, bool wide, bo
     p.U = static_cast<int64_t>(p.T) * p.G;
     p.P = static_cast<int>(p.U < static_cast<int64_t>(cus) * occ ? p.U : static_cast<int64_t>(cus) * occ);
     p.slot_floats = decode_slot_floats(p.MT, p.S);
-  } else if (wide && !tn.wide_off && M >= (tn.wide_min_m > 0 ? tn.wide_min_m : 256) &&
-             2 * cdiv(M, 256) * cdiv(N, 256) >= cus) {
-    // 256x256 tiles need about one tile per two CUs: with fewer, most tiles
-    // are split across many workgroups and their 256 KB fp32 partials cost
-    // more than the bigger tiles save (down 17408->5120 at 512 rows: 382 us
-    // vs 191 us for 128-row tiles).
+  } else if (wide && !tn.wide_off && M >= (tn.wide_min_m > 0 ? tn.wide_min_m : 129)) {
+    // With coherent 16-byte partial loads the 256x256 tiles win even where
+    // few tiles exist and most are split (down 17408->5120 at 512 rows:
+    // 139 us vs 218 us for 128-row tiles).
     p.decode = false;
     p.wide = true;
     p.TM = static_cast<int>(cdiv(M, 256));

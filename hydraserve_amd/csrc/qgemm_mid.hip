@@ -1,9 +1,9 @@
-// Decode-regime (17..64 activation rows) quantized weight GEMM for gfx950:
+// Decode-regime (17..128 activation rows) quantized weight GEMM for gfx950:
 // an LDS-DMA streamer feeding 32x32 MFMA tiles.
 //
 // Replaces the Triton launches of hydraserve/kernels/awq.py:52-74
 // (_awq_gemm_kernel, awq.py:82-142) and hydraserve/kernels/fp8.py:68-96
-// (_fp8_gemm_kernel, fp8.py:104-168) for activations of 17..64 rows, where
+// (_fp8_gemm_kernel, fp8.py:104-168) for activations of 17..128 rows, where
 // the weight stream is still the roofline but every weight feeds 32-64
 // output rows.
 //
@@ -470,10 +470,10 @@ static hipError_t launch_mid_t(const GemmArgs& a, hipStream_t stream) {
 
 int mid_slot_floats(int bmi, int nj, int nw) { return nw * bmi * nj * 1024; }
 
-// K a multiple of 128, 16-byte aligned rows, M <= 64, every buffer byte
+// K a multiple of 128, 16-byte aligned rows, M <= 128, every buffer byte
 // offset below 2^31.
 bool mid_ok(const GemmArgs& a, int wt) {
-  if (a.M <= 0 || a.M > 64 || a.N <= 0 || a.K <= 0 || a.K % 128 != 0 || !a.xvec || !a.wvec) return false;
+  if (a.M <= 0 || a.M > 128 || a.N <= 0 || a.K <= 0 || a.K % 128 != 0 || !a.xvec || !a.wvec) return false;
   const int64_t lim = int64_t(1) << 31;
   const int64_t xb = (static_cast<int64_t>(a.M) * a.ldx + a.K) * 2;
   const int64_t wb = (static_cast<int64_t>(a.N) + 256) * a.ldw * (wt == W_INT4 ? 4 : 1);
@@ -492,6 +492,14 @@ static hipError_t launch_mid_s(const GemmArgs& a, int bmi, int nj, int nw, hipSt
   if (bmi == 1 && nj == 2) return launch_mid_t<WT, SDT, 1, 2, 4>(a, stream);
   if (bmi == 2 && nj == 1) return launch_mid_t<WT, SDT, 2, 1, 4>(a, stream);
   if (bmi == 2 && nj == 2) return launch_mid_t<WT, SDT, 2, 2, 4>(a, stream);
+  if (bmi == 3 && nj == 1) return launch_mid_t<WT, SDT, 3, 1, 4>(a, stream);
+  if (bmi == 4 && nj == 1) return launch_mid_t<WT, SDT, 4, 1, 4>(a, stream);
+  if constexpr (WT == W_INT4) {
+    // FP8 weights double the slot's weight bytes: 3-4 row blocks with two
+    // column blocks per wave would not fit the LDS ring.
+    // (4 row blocks x 2 column blocks would spill.)
+    if (bmi == 3 && nj == 2) return launch_mid_t<WT, SDT, 3, 2, 4>(a, stream);
+  }
   return hipErrorInvalidValue;
 }
 
