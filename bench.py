@@ -85,7 +85,7 @@ def make_fp8(torch, n, k, copies, gen, dev):
 # `bench.py --profile KIND:SHAPE:M` (KiB per dispatch), scaled by what the same
 # counters read for a 512 MiB copy: FETCH x2.0, WRITE x1.0.  Kept beside the
 # summaries under profiles/; shapes not listed report null.
-PMC_TRAFFIC_KIB = {("int4", "gate_up", 64): (60180.5, 19728.5)}
+PMC_TRAFFIC_KIB = {("int4", "gate_up", 64): (69799.2, 28954.0)}
 FETCH_CAL, WRITE_CAL = 2.0, 1.0
 
 

@@ -53,6 +53,7 @@ struct Tuning {
   int rows_off = 0;        // 1: never use the row-partitioned decode kernel
   int rows_wg = 0;         // its workgroups per CU (0 = 1)
   int rows_xl = 1;         // 0: never stage X in LDS (read A fragments from global memory)
+  int rows_force = 0;      // 1: use it whenever it can run
   int gemv_off = 0;        // 1: never use the block-major kernel
   int gemv_kw = 0;         // its wavefronts per workgroup (0 = 8)
   int gemv_wg = 0;         // its workgroups per CU (0 = 1)
@@ -85,6 +86,7 @@ const Tuning& tuning() {
     r.rows_off = env_int("HS_ROWS_OFF");
     r.rows_wg = env_int("HS_ROWS_WG");
     if (std::getenv("HS_ROWS_XL") != nullptr) r.rows_xl = env_int("HS_ROWS_XL");
+    r.rows_force = env_int("HS_ROWS_FORCE");
     rows_kw8 = env_int("HS_ROWS_KW8");
     r.gemv_off = env_int("HS_GEMV_OFF");
     r.gemv_kw = env_int("HS_GEMV_KW");
@@ -260,9 +262,10 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
     const int P = device_cus() * (tn.rows_wg > 0 ? tn.rows_wg : 1);
     int nblk = 0;
     bool xl = false;
-    // Above 4 rows with narrow partitions (1-2 blocks of 16 weight rows per
-    // workgroup) the streaming kernel below is faster.
-    if (rows_ok(a, wt, P, &nblk, &xl, tn.rows_xl) && (a.M <= 4 || nblk >= 3)) {
+    // Above 4 rows (8 for INT4) with narrow partitions (1-2 blocks of 16
+    // weight rows per workgroup) the streaming kernel below is faster.
+    if (rows_ok(a, wt, P, &nblk, &xl, tn.rows_xl) &&
+        (tn.rows_force || a.M <= 4 || (a.M <= 8 && wt == W_INT4) || nblk >= 3)) {
       a.P = P;
       a.T = a.K / 128;
       return hip_code(launch_rows(wt, a, nblk, xl, stream));
