@@ -177,7 +177,11 @@ struct Mid {
   }
 
   // Fragment (column block j, step t): 8 weights of the lane's row.
-  static __device__ __forceinline__ bf16x8_t decode(const Raw& r, int j, int t, int l32) {
+  // nib_mask = 0x000F000F and magic = 0x64006400 arrive as registers the
+  // compiler cannot fold, so each output dword is one shift and one
+  // v_and_or_b32 rather than a shift, an AND and an OR with literals.
+  static __device__ __forceinline__ bf16x8_t decode(const Raw& r, int j, int t, int l32, uint32_t nib_mask,
+                                                    uint32_t magic) {
     u32x4_t p;
     float s;
     if constexpr (SDT == SCALE_F32) {
@@ -195,7 +199,7 @@ struct Mid {
       float f[8];
 #pragma unroll
       for (int sh = 0; sh < 4; ++sh) {
-        const f16x2_t v = __builtin_bit_cast(f16x2_t, ((w >> (4 * sh)) & 0x000F000Fu) | 0x64006400u);
+        const f16x2_t v = __builtin_bit_cast(f16x2_t, insert_nibbles(nib_mask, w >> (4 * sh), magic));
         if constexpr (SDT == SCALE_F32) {
           f[sh] = (static_cast<float>(v[0]) - c) * s;
           f[sh + 4] = (static_cast<float>(v[1]) - c) * s;
@@ -346,6 +350,8 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_mid_kernel(GemmArgs a) {
   uint32_t aoff[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) aoff[t] = l32 * 128 + (((4 * h + t) ^ ((l32 >> 1) & 7)) * 16);
+  const uint32_t nib_mask = opaque_and(0x000F000Fu, 0xFFFFFFFFu);
+  const uint32_t magic = opaque_and(0x64006400u, 0xFFFFFFFFu);
 
   // DMA cursor: the next unit to load (tile dt, chunk dc), advanced without
   // divisions and held at the range's last unit once the range is exhausted
@@ -387,7 +393,7 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_mid_kernel(GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < BMI; ++i) A[i] = K::read_a(sm, 0, aoff[0], i);
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) B[j] = K::decode(r0, j, 0, l32);
+  for (int j = 0; j < NJ; ++j) B[j] = K::decode(r0, j, 0, l32, nib_mask, magic);
 
   // One unit k (slot k % D): at entry A, B hold its step 0 and Rc its raw
   // data; at exit A, B hold step 0 of unit k+1 and Rn its raw data.
@@ -417,7 +423,7 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_mid_kernel(GemmArgs a) {
 #pragma unroll
       for (int i = 0; i < BMI; ++i) An[i] = t < 3 ? K::read_a(sm, sc, aoff[t + 1], i) : K::read_a(sm, sn, aoff[0], i);
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) Bn[j] = t < 3 ? K::decode(Rc, j, t + 1, l32) : K::decode(Rn, j, 0, l32);
+      for (int j = 0; j < NJ; ++j) Bn[j] = t < 3 ? K::decode(Rc, j, t + 1, l32, nib_mask, magic) : K::decode(Rn, j, 0, l32, nib_mask, magic);
 #pragma unroll
       for (int i = 0; i < BMI; ++i)
 #pragma unroll

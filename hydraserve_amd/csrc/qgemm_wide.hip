@@ -175,7 +175,10 @@ struct Wide {
 
   // Fragment (row half j, step t) of the next unit: 8 weights of the lane's
   // row in K order.
-  static __device__ __forceinline__ bf16x8_t decode(const Raw& r, const uint32_t (&zsh)[2], int j, int t) {
+  // nib_mask = 0x000F000F and magic = 0x64006400 arrive as registers the
+  // compiler cannot fold: one shift and one v_and_or_b32 per output dword.
+  static __device__ __forceinline__ bf16x8_t decode(const Raw& r, const uint32_t (&zsh)[2], int j, int t,
+                                                    uint32_t nib_mask, uint32_t magic) {
     u32x4_t p;
     const u32x4_t* q = j == 0 ? r.q0 : r.q1;
     const uint32_t sb = j == 0 ? r.s0 : r.s1;
@@ -197,7 +200,7 @@ struct Wide {
       float f[8];
 #pragma unroll
       for (int sh = 0; sh < 4; ++sh) {
-        const f16x2_t v = __builtin_bit_cast(f16x2_t, ((w >> (4 * sh)) & 0x000F000Fu) | 0x64006400u);
+        const f16x2_t v = __builtin_bit_cast(f16x2_t, insert_nibbles(nib_mask, w >> (4 * sh), magic));
         if constexpr (SDT == SCALE_F32) {
           f[sh] = (static_cast<float>(v[0]) - c) * s;
           f[sh + 4] = (static_cast<float>(v[1]) - c) * s;
@@ -239,7 +242,7 @@ struct Wide {
   static __device__ __forceinline__ void unit(Smem& sm, int bc, int bn, int bd, int cnext2, bf16x8_t (&A)[MI],
                                               bf16x8_t (&B)[2], Raw& Rc, const Raw& Rn, const Rsrc& rs,
                                               const Offs& o, const uint32_t (&aoff)[4], f32x16_t (&acc)[MI][2],
-                                              int wave) {
+                                              int wave, uint32_t nm, uint32_t mg) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       if (t == 3) {
@@ -252,7 +255,7 @@ struct Wide {
 #pragma unroll
       for (int i = 0; i < MI; ++i) An[i] = t < 3 ? read_a(sm, bc, aoff[t + 1], i) : read_a(sm, bn, aoff[0], i);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) Bn[j] = t < 3 ? decode(Rc, o.zsh, j, t + 1) : decode(Rn, o.zsh, j, 0);
+      for (int j = 0; j < 2; ++j) Bn[j] = t < 3 ? decode(Rc, o.zsh, j, t + 1, nm, mg) : decode(Rn, o.zsh, j, 0, nm, mg);
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[i], B[0], acc[i][0], 0, 0, 0);
@@ -400,6 +403,8 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
   uint32_t aoff[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) aoff[t] = l32 * 128 + (((4 * h + t) ^ ((l32 >> 1) & 7)) * 16);
+  const uint32_t nm = opaque_and(0x000F000Fu, 0xFFFFFFFFu);
+  const uint32_t mg = opaque_and(0x64006400u, 0xFFFFFFFFu);
 
   int64_t u = u0;
   while (u < u1) {
@@ -426,8 +431,8 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
     bf16x8_t A[W::MI], B[2];
 #pragma unroll
     for (int i = 0; i < W::MI; ++i) A[i] = W::read_a(sm, 0, aoff[0], i);
-    B[0] = W::decode(r0, o.zsh, 0, 0);
-    B[1] = W::decode(r0, o.zsh, 1, 0);
+    B[0] = W::decode(r0, o.zsh, 0, 0, nm, mg);
+    B[1] = W::decode(r0, o.zsh, 1, 0, nm, mg);
 
     f32x16_t acc[W::MI][2];
 #pragma unroll
@@ -444,7 +449,7 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
     int q = 0;
     if (n & 1) {
       const int cn = cb + 2 < ce ? cb + 2 : ce - 1;
-      W::unit(sm, b0, b1, b2, cn, A, B, r0, r1, rs, o, aoff, acc, wave);
+      W::unit(sm, b0, b1, b2, cn, A, B, r0, r1, rs, o, aoff, acc, wave, nm, mg);
       const int tb = b0;
       b0 = b1;
       b1 = b2;
@@ -457,8 +462,8 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
     for (; q < n; q += 2) {
       const int cn0 = cb + q + 2 < ce ? cb + q + 2 : ce - 1;
       const int cn1 = cb + q + 3 < ce ? cb + q + 3 : ce - 1;
-      W::unit(sm, b0, b1, b2, cn0, A, B, r0, r1, rs, o, aoff, acc, wave);
-      W::unit(sm, b1, b2, b0, cn1, A, B, r1, r0, rs, o, aoff, acc, wave);
+      W::unit(sm, b0, b1, b2, cn0, A, B, r0, r1, rs, o, aoff, acc, wave, nm, mg);
+      W::unit(sm, b1, b2, b0, cn1, A, B, r1, r0, rs, o, aoff, acc, wave, nm, mg);
       const int tb = b0;
       b0 = b2;
       b2 = b1;
