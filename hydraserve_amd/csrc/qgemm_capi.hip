@@ -70,7 +70,6 @@ struct Tuning {
   int mid_off = 0;         // 1: never use the LDS-DMA streaming kernel for 17..64 rows
   int mid_min_m = 0;       // smallest M for it (0 = 17)
   int mid_nj = 0;          // its 32-column blocks per wave (0 = heuristic)
-  int mid_nw = 0;          // its wavefronts per workgroup (0 = heuristic)
   int prefill_wg_per_cu = 0;
 };
 
@@ -105,7 +104,6 @@ const Tuning& tuning() {
     r.mid_off = env_int("HS_MID_OFF");
     r.mid_min_m = env_int("HS_MID_MIN_M");
     r.mid_nj = env_int("HS_MID_NJ");
-    r.mid_nw = env_int("HS_MID_NW");
     r.prefill_wg_per_cu = env_int("HS_PREFILL_WG_PER_CU");
     return r;
   }();
@@ -158,14 +156,7 @@ Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast, bool wide, bo
     // enough tiles exist and fewer of them are split across workgroups.
     p.NJ = tn.mid_nj == 1 || tn.mid_nj == 2 ? tn.mid_nj : (N >= 16384 ? 2 : 1);
     if ((wt != W_INT4 && p.BMI > 2) || p.BMI > 3) p.NJ = 1;
-    // 8 waves of one column block each (two waves per SIMD, 33..64 rows)
-    // measured no faster than 4 waves of two: the SIMDs' VALU and MFMA work
-    // per unit is the same either way.
-    p.NW = tn.mid_nw == 4 || tn.mid_nw == 8 ? tn.mid_nw : 4;
-    if (p.NW == 8) {
-      if (p.BMI != 2) p.NW = 4;  // the 8-wave layout is built for 2 row blocks only
-      else p.NJ = 1;
-    }
+    p.NW = 4;
     p.T = static_cast<int>(cdiv(N, 32 * p.NJ * p.NW));
     p.G = K / 64;
     p.U = static_cast<int64_t>(p.T) * p.G;

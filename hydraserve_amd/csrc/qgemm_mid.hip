@@ -7,12 +7,12 @@
 // the weight stream is still the roofline but every weight feeds 32-64
 // output rows.
 //
-//   * A workgroup (NW = 4 or 8 wavefronts) owns a BM x BN output tile,
+//   * A workgroup (NW = 4 wavefronts) owns a BM x BN output tile,
 //     BM = 32*BMI rows (all of M), BN = 32*NJ*NW weight rows; wave w owns
 //     weight rows [32*NJ*w, +32*NJ): BMI x NJ blocks of 32x32 fp32
-//     accumulators.  With 8 waves each holds half the registers and two
-//     share every SIMD, so one wave's LDS and VALU latency hides behind the
-//     other's work.
+//     accumulators.  (8 waves of one column block each -- two per SIMD --
+//     measured no faster: per unit, each SIMD's VALU and MFMA work is the
+//     same either way.)
 //   * K advances 64 per unit; units are scheduled stream-K over a persistent
 //     grid.  Everything a unit needs -- the X tile [BM x 64] (shared by the
 //     four waves), each wave's packed weights, scales and (INT4) zero-point
@@ -490,10 +490,7 @@ bool mid_ok(const GemmArgs& a, int wt) {
 
 template <int WT, int SDT>
 static hipError_t launch_mid_s(const GemmArgs& a, int bmi, int nj, int nw, hipStream_t stream) {
-  if (nw == 8) {
-    if (bmi == 2 && nj == 1) return launch_mid_t<WT, SDT, 2, 1, 8>(a, stream);
-    return hipErrorInvalidValue;
-  }
+  if (nw != 4) return hipErrorInvalidValue;
   if (bmi == 1 && nj == 1) return launch_mid_t<WT, SDT, 1, 1, 4>(a, stream);
   if (bmi == 1 && nj == 2) return launch_mid_t<WT, SDT, 1, 2, 4>(a, stream);
   if (bmi == 2 && nj == 1) return launch_mid_t<WT, SDT, 2, 1, 4>(a, stream);

@@ -417,11 +417,17 @@ def _sampled_columns(rng, n, count=48):
     return np.sort(np.concatenate([cols, [0, n - 1]]))
 
 
-@pytest.mark.parametrize("m", [1, 4, 16, 64, 512])
-@pytest.mark.parametrize("n,k", [(34816, 5120), (5120, 17408)])
+CONFIG4_SHAPES = [(10240, 5120), (5120, 8192), (12288, 5120)]  # qkv, o_proj, GDN in_proj (N, K)
+
+
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(m, n, k) for m in (1, 4, 16, 64, 128, 512, 2048) for n, k in ((34816, 5120), (5120, 17408))]
+    + [(m, n, k) for m in (64, 1024) for n, k in CONFIG4_SHAPES],
+)
 def test_int4_baseline_shapes_sampled_oracle(m, n, k):
-    """Full-size configs 1/2: uniform random packed words (uniform nibbles) on the
-    GPU; the oracle recomputes 50 sampled output columns exactly."""
+    """Full-size configs 1, 2 and 4: uniform random packed words (uniform
+    nibbles) on the GPU; the oracle recomputes 50 sampled output columns."""
     dev = _cuda()
     g = torch.Generator(device="cpu").manual_seed(m + n)
     kw, groups = k // 8, k // 128
@@ -442,7 +448,7 @@ def test_int4_baseline_shapes_sampled_oracle(m, n, k):
     assert_gemm_close(y[:, cols], ref, what=f"m={m} {n}x{k}")
 
 
-@pytest.mark.parametrize("m", [1, 16, 256])
+@pytest.mark.parametrize("m", [1, 16, 64, 256, 2048])
 @pytest.mark.parametrize("n,k", [(34816, 5120), (5120, 17408)])
 def test_fp8_baseline_shapes_sampled_oracle(m, n, k):
     dev = _cuda()
