@@ -28,8 +28,8 @@ int mid_slot_floats(int bmi, int nj, int nw);
 bool mid_ok(const GemmArgs& a, int wt);
 int wide_slot_floats();
 bool wide_ok(const GemmArgs& a, int wt);
-bool rows_ok(const GemmArgs& a, int wt, int P, int* nblk_out, bool* xl_out, int xl_pref);
-hipError_t launch_rows(int wt, const GemmArgs& a, int nblk, bool xl, hipStream_t stream);
+bool rows_ok(const GemmArgs& a, int wt, int P, int* nblk_out, bool* xl_out, int* ms_out, int xl_pref);
+hipError_t launch_rows(int wt, const GemmArgs& a, int nblk, bool xl, int ms, hipStream_t stream);
 extern int rows_kw8;
 bool gemv_ok(const GemmArgs& a, int wt, int P, int kw_pref, int* kw_out, int* rows_max);
 hipError_t launch_gemv(int wt, const GemmArgs& a, int kw, hipStream_t stream);
@@ -70,6 +70,7 @@ struct Tuning {
   int mid_off = 0;         // 1: never use the LDS-DMA streaming kernel for 17..64 rows
   int mid_min_m = 0;       // smallest M for it (0 = 17)
   int mid_nj = 0;          // its 32-column blocks per wave (0 = heuristic)
+  int rows_ms2_off = 0;    // 1: the row-partitioned kernel only up to 16 rows
   int prefill_wg_per_cu = 0;
 };
 
@@ -104,6 +105,7 @@ const Tuning& tuning() {
     r.mid_off = env_int("HS_MID_OFF");
     r.mid_min_m = env_int("HS_MID_MIN_M");
     r.mid_nj = env_int("HS_MID_NJ");
+    r.rows_ms2_off = env_int("HS_ROWS_MS2_OFF");
     r.prefill_wg_per_cu = env_int("HS_PREFILL_WG_PER_CU");
     return r;
   }();
@@ -249,17 +251,18 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
       return hip_code(launch_gemv(wt, a, kw, stream));
     }
   }
-  if (!tn.rows_off && a.M <= 16) {
+  if (!tn.rows_off && a.M <= (tn.rows_ms2_off ? 16 : 32)) {
     const int P = device_cus() * (tn.rows_wg > 0 ? tn.rows_wg : 1);
-    int nblk = 0;
+    int nblk = 0, ms = 1;
     bool xl = false;
     // Above 4 rows (8 for INT4) with narrow partitions (1-2 blocks of 16
-    // weight rows per workgroup) the streaming kernel below is faster.
-    if (rows_ok(a, wt, P, &nblk, &xl, tn.rows_xl) &&
+    // weight rows per workgroup) the streaming kernel below is faster;
+    // 17..32 rows take two 16-row strips and need 3+ row blocks.
+    if (rows_ok(a, wt, P, &nblk, &xl, &ms, tn.rows_xl) &&
         (tn.rows_force || a.M <= 4 || (a.M <= 8 && wt == W_INT4) || nblk >= 3)) {
       a.P = P;
       a.T = a.K / 128;
-      return hip_code(launch_rows(wt, a, nblk, xl, stream));
+      return hip_code(launch_rows(wt, a, nblk, xl, ms, stream));
     }
   }
   const int nb = tn.st_nb > 0 ? tn.st_nb : stream_nb(a.M);

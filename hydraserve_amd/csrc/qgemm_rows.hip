@@ -1,8 +1,10 @@
-// Decode-regime (M <= 16) quantized weight GEMM for gfx950: row-partitioned.
+// Decode-regime (M <= 32) quantized weight GEMM for gfx950: row-partitioned.
 //
 // Replaces the Triton launches of hydraserve/kernels/awq.py:52-74
 // (_awq_gemm_kernel, awq.py:82-142) and hydraserve/kernels/fp8.py:68-96
-// (_fp8_gemm_kernel, fp8.py:104-168) for activations of at most 16 rows.
+// (_fp8_gemm_kernel, fp8.py:104-168) for activations of at most 16 rows
+// (MS = 1 strip) and, on wide outputs, 17..32 rows (MS = 2 strips of 16
+// rows sharing every unpacked weight fragment).
 //
 // Work split.  Workgroup p owns the contiguous weight rows
 // [p*N/P, (p+1)*N/P) -- at most 16*NBLK rows, NBLK blocks of 16 -- and its KW
@@ -16,7 +18,8 @@
 // Per wavefront, per chunk c of its range:
 //   * weights: lane (l16, h) holds 16 bytes (INT4) / 32 bytes (FP8) of row
 //     16b + l16 of every block b -- one buffer load per block;
-//   * A fragments: the same lane holds X[min(l16, M-1)][c*128 + 32h, +32),
+//   * A fragments: the same lane holds X[min(16s + l16, M-1)][c*128 + 32h, +32)
+//     for each strip s,
 //     either from a copy of X staged into LDS once (XL: when X fits) or read
 //     from global memory (an L2 hit after first use) two groups ahead;
 //   * weights stream through a register ring RD chunks deep: the slot of a
@@ -35,7 +38,7 @@
 
 namespace hsq {
 
-template <int WT, int SDT, int NBLK, int KW, int RD, bool XL>
+template <int WT, int SDT, int NBLK, int KW, int RD, bool XL, int MS>
 struct RowsK {
   static constexpr int THREADS = 64 * KW;
   static constexpr int SES = SDT == SCALE_F32 ? 4 : 2;
@@ -46,7 +49,7 @@ struct RowsK {
     u32x4_t q[NBLK][LPB];
   };
   struct ASlot {
-    u32x4_t a[4];
+    u32x4_t a[MS][4];
   };
 
   // LDS: [front] the reduction area ([KW][NBLK][64 lanes] f32x4), which for
@@ -54,7 +57,7 @@ struct RowsK {
   // rows over the banks); then zero points (INT4: rows r0>>3 .. (r1-1)>>3,
   // GC words each); then scales (INT4: one row per weight row; FP8: one row
   // per 128-row block), GC entries each.
-  static __host__ __device__ int red_bytes() { return KW * NBLK * 64 * 16; }
+  static __host__ __device__ int red_bytes() { return KW * NBLK * MS * 64 * 16; }
   static __host__ __device__ int x_stride(int K) { return 2 * K + 32; }
   static __host__ __device__ size_t front_bytes(int M, int K) {
     const size_t x = XL ? static_cast<size_t>(M) * x_stride(K) : 0;
@@ -82,9 +85,9 @@ struct RowsK {
 };
 
 // a.P = workgroups (row partitions); a.T = chunks per row (K / 128).
-template <int WT, int SDT, int NBLK, int KW, int RD, bool XL>
+template <int WT, int SDT, int NBLK, int KW, int RD, bool XL, int MS>
 __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
-  using D = RowsK<WT, SDT, NBLK, KW, RD, XL>;
+  using D = RowsK<WT, SDT, NBLK, KW, RD, XL, MS>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int GC = a.T;
   const int tid = threadIdx.x;
@@ -130,9 +133,14 @@ __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
       zsh[b] = 0;
     }
   }
-  const int xm = l16 < a.M ? l16 : a.M - 1;
-  const uint32_t xoff = static_cast<uint32_t>(xm * static_cast<int>(a.ldx) * 2) + 64u * h;
-  const uint32_t xloff = static_cast<uint32_t>(xm * xst) + 64u * h;
+  // Activation row of the lane in strip s (rows past M repeat row M-1).
+  uint32_t xoff[MS], xloff[MS];
+#pragma unroll
+  for (int s = 0; s < MS; ++s) {
+    const int xm = 16 * s + l16 < a.M ? 16 * s + l16 : a.M - 1;
+    xoff[s] = static_cast<uint32_t>(xm * static_cast<int>(a.ldx) * 2) + 64u * h;
+    xloff[s] = static_cast<uint32_t>(xm * xst) + 64u * h;
+  }
 
   const uint32_t nib_mask = opaque_and(0x000F000Fu, 0xFFFFFFFFu);
   const uint32_t magic = opaque_and(0x43004300u, 0xFFFFFFFFu);
@@ -153,7 +161,9 @@ __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
   auto load_a = [&](typename D::ASlot& as, int i) __attribute__((always_inline)) {
     const uint32_t xs = static_cast<uint32_t>(chunk_of(i) * 256);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) as.a[j] = bload<u32x4_t>(rx, xoff + 16u * j, xs);
+    for (int s = 0; s < MS; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) as.a[s][j] = bload<u32x4_t>(rx, xoff[s] + 16u * j, xs);
   };
 
   // Weights: a ring of RD chunks (slot r = chunk % RD), refilled block by
@@ -211,9 +221,11 @@ __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
   }
   __syncthreads();
 
-  f32x4_t acc[NBLK];
+  f32x4_t acc[NBLK][MS];
 #pragma unroll
-  for (int b = 0; b < NBLK; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < NBLK; ++b)
+#pragma unroll
+    for (int s = 0; s < MS; ++s) acc[b][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // One group of RD chunks starting at chunk i0 (A fragments in abuf[G]
   // without XL).
@@ -228,28 +240,37 @@ __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
       const int i = i0 + r;
       const bool valid = i < n;
       const int c = cs + (valid ? i : n - 1);
-      bf16x8_t A[4];
+      bf16x8_t A[MS][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if constexpr (XL) {
-          A[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(xl + xloff + c * 256 + 16 * j));
-        } else if constexpr (WT == W_INT4) {
-          A[j] = __builtin_bit_cast(bf16x8_t, permute_x(abuf[G][r].a[j]));
-        } else {
-          A[j] = __builtin_bit_cast(bf16x8_t, abuf[G][r].a[j]);
+      for (int s = 0; s < MS; ++s)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (XL) {
+            A[s][j] =
+                __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(xl + xloff[s] + c * 256 + 16 * j));
+          } else if constexpr (WT == W_INT4) {
+            A[s][j] = __builtin_bit_cast(bf16x8_t, permute_x(abuf[G][r].a[s][j]));
+          } else {
+            A[s][j] = __builtin_bit_cast(bf16x8_t, abuf[G][r].a[s][j]);
+          }
         }
-      }
-      f32x4_t xg = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (WT == W_INT4) {
+      f32x4_t xg[MS];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[j], ones, xg, 0, 0, 0);
+      for (int s = 0; s < MS; ++s) {
+        xg[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if constexpr (WT == W_INT4) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) xg[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[s][j], ones, xg[s], 0, 0, 0);
+        }
       }
       // Software pipeline over the blocks.  Region b: unpack block b, refill
       // block b-1's slot (its only reader was the previous region's unpack),
       // multiply block b, fold block b-1's products.  Nothing in a region
       // depends on another of its parts, so the scheduler interleaves them;
       // the barrier between regions keeps every refill after its slot's read.
-      f32x4_t tp = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t tp[MS];
+#pragma unroll
+      for (int s = 0; s < MS; ++s) tp[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int b = 0; b <= NBLK; ++b) {
         bf16x8_t B[4];
@@ -264,10 +285,14 @@ __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
           }
         }
         if (b > 0) load_w(wring[r].q[b - 1], b - 1, i + RD);
-        f32x4_t t = {0.f, 0.f, 0.f, 0.f};
-        if (b < NBLK) {
+        f32x4_t t[MS];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[j], B[j], t, 0, 0, 0);
+        for (int s = 0; s < MS; ++s) {
+          t[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          if (b < NBLK) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) t[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[s][j], B[j], t[s], 0, 0, 0);
+          }
         }
         if (b > 0) {
           const int bb = b - 1;
@@ -275,13 +300,18 @@ __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
           if constexpr (WT == W_INT4) {
             const float negc = -(128.0f + static_cast<float>((zl[zoff[bb] + c] >> zsh[bb]) & 0xFu));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[bb][e] = fmaf(sc, fmaf(negc, xg[e], tp[e]), acc[bb][e]);
+            for (int s = 0; s < MS; ++s)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[bb][s][e] = fmaf(sc, fmaf(negc, xg[s][e], tp[s][e]), acc[bb][s][e]);
           } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[bb][e] = fmaf(sc, tp[e], acc[bb][e]);
+            for (int s = 0; s < MS; ++s)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[bb][s][e] = fmaf(sc, tp[s][e], acc[bb][s][e]);
           }
         }
-        tp = t;
+#pragma unroll
+        for (int s = 0; s < MS; ++s) tp[s] = t[s];
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -298,50 +328,58 @@ __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
 
   // ---- reduce the KW partial sums of every output, in wavefront order ---------
   if constexpr (XL) __syncthreads();  // the reduction area overlays X
+  // Entry (w, b, s) of the reduction area: wavefront w's sums of block b,
+  // strip s.  Work item i = b * MS + s is reduced by wavefront i % KW.
 #pragma unroll
   for (int b = 0; b < NBLK; ++b)
-    *reinterpret_cast<f32x4_t*>(red + ((wave * NBLK + b) * 64 + lane) * 4) = acc[b];
+#pragma unroll
+    for (int s = 0; s < MS; ++s)
+      *reinterpret_cast<f32x4_t*>(red + (((wave * NBLK + b) * MS + s) * 64 + lane) * 4) = acc[b][s];
   __syncthreads();
-  for (int b = wave; b < NBLK; b += KW) {
-    f32x4_t s = *reinterpret_cast<const f32x4_t*>(red + ((0 * NBLK + b) * 64 + lane) * 4);
+  for (int i = wave; i < NBLK * MS; i += KW) {
+    const int b = i / MS, s = i - b * MS;
+    f32x4_t sum = *reinterpret_cast<const f32x4_t*>(red + (i * 64 + lane) * 4);
 #pragma unroll
     for (int w = 1; w < KW; ++w) {
-      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(red + ((w * NBLK + b) * 64 + lane) * 4);
-      s[0] += v[0];
-      s[1] += v[1];
-      s[2] += v[2];
-      s[3] += v[3];
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(red + ((w * NBLK * MS + i) * 64 + lane) * 4);
+      sum[0] += v[0];
+      sum[1] += v[1];
+      sum[2] += v[2];
+      sum[3] += v[3];
     }
     const int rl = 16 * b + l16;
     if (rl < nr) {
       const int col = r0 + rl;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int m = 4 * h + e;
-        if (m < a.M) a.y[m * a.ldy + col] = to_bf16_bits(s[e]);
+        const int m = 16 * s + 4 * h + e;
+        if (m < a.M) a.y[m * a.ldy + col] = to_bf16_bits(sum[e]);
       }
     }
   }
 }
 
-template <int WT, int SDT, int NBLK, int KW, int RD, bool XL>
+template <int WT, int SDT, int NBLK, int KW, int RD, bool XL, int MS>
 static hipError_t launch_rows_t(const GemmArgs& a, hipStream_t stream) {
-  using D = RowsK<WT, SDT, NBLK, KW, RD, XL>;
+  using D = RowsK<WT, SDT, NBLK, KW, RD, XL, MS>;
   const size_t lds = D::lds_bytes(a.M, a.K);
-  hipLaunchKernelGGL((qgemm_rows_kernel<WT, SDT, NBLK, KW, RD, XL>), dim3(a.P), dim3(D::THREADS), lds, stream, a);
+  hipLaunchKernelGGL((qgemm_rows_kernel<WT, SDT, NBLK, KW, RD, XL, MS>), dim3(a.P), dim3(D::THREADS), lds, stream, a);
   return hipGetLastError();
 }
 
 // K split and ring depth for NBLK row blocks: 8-16 KB of weight loads in
 // flight per wavefront within the register budget (FP8 chunks are twice the
 // bytes of INT4 chunks; staging X in LDS frees the A-fragment registers).
+// Two 16-row strips (17..32 activation rows) run only with 3+ row blocks,
+// without XL, at the one-chunk ring.
 struct RowsCfg {
   int nblk, kw, rd;
 };
 
 int rows_kw8 = 0;  // tuning: 1 selects 8 wavefronts (2 per SIMD) for INT4 with 5+ row blocks
 
-static RowsCfg rows_cfg(int wt, int nblk, bool xl) {
+static RowsCfg rows_cfg(int wt, int nblk, bool xl, int ms) {
+  if (ms > 1) return {nblk, 4, 1};
   if (wt == W_INT4) {
     if (nblk <= 2) return {nblk, 8, 4};
     if (nblk <= 4) return {nblk, 4, xl ? 4 : 2};
@@ -354,11 +392,20 @@ static RowsCfg rows_cfg(int wt, int nblk, bool xl) {
 }
 
 #define HSQ_RW(NB_, KW_, RD_) \
-  if (c.nblk == NB_ && c.kw == KW_ && c.rd == RD_) return launch_rows_t<WT, SDT, NB_, KW_, RD_, XL>(a, stream);
+  if (c.nblk == NB_ && c.kw == KW_ && c.rd == RD_) return launch_rows_t<WT, SDT, NB_, KW_, RD_, XL, 1>(a, stream);
+#define HSQ_RW2(NB_) \
+  if (c.nblk == NB_) return launch_rows_t<WT, SDT, NB_, 4, 1, false, 2>(a, stream);
 
 template <int WT, int SDT, bool XL>
-static hipError_t launch_rows_x(const GemmArgs& a, int nblk, hipStream_t stream) {
-  const RowsCfg c = rows_cfg(WT, nblk, XL);
+static hipError_t launch_rows_x(const GemmArgs& a, int nblk, int ms, hipStream_t stream) {
+  const RowsCfg c = rows_cfg(WT, nblk, XL, ms);
+  if (ms == 2) {
+    if constexpr (!XL) {
+      HSQ_RW2(3) HSQ_RW2(4) HSQ_RW2(5) HSQ_RW2(6) HSQ_RW2(7) HSQ_RW2(8) HSQ_RW2(9)
+    }
+    return hipErrorInvalidValue;
+  }
+  if (ms != 1) return hipErrorInvalidValue;
   if constexpr (WT == W_INT4 && XL) {
     HSQ_RW(1, 8, 4) HSQ_RW(2, 8, 4) HSQ_RW(3, 4, 4) HSQ_RW(4, 4, 4) HSQ_RW(5, 4, 2) HSQ_RW(6, 4, 2)
     HSQ_RW(7, 4, 2) HSQ_RW(8, 4, 2) HSQ_RW(9, 4, 2)
@@ -377,14 +424,15 @@ static hipError_t launch_rows_x(const GemmArgs& a, int nblk, hipStream_t stream)
   return hipErrorInvalidValue;
 }
 #undef HSQ_RW
+#undef HSQ_RW2
 
 constexpr int kRowsMaxBlocks = 9;
 constexpr size_t kRowsMaxLds = 160 * 1024;
 
-size_t rows_lds_bytes(int wt, int sdt, int nblk, bool xl, int M, int K) {
-  const RowsCfg c = rows_cfg(wt, nblk, xl);
+size_t rows_lds_bytes(int wt, int sdt, int nblk, bool xl, int M, int K, int ms) {
+  const RowsCfg c = rows_cfg(wt, nblk, xl, ms);
   const int GC = K / 128;
-  const size_t red = static_cast<size_t>(c.kw) * c.nblk * 64 * 16;
+  const size_t red = static_cast<size_t>(c.kw) * c.nblk * ms * 64 * 16;
   const size_t x = xl ? static_cast<size_t>(M) * (2 * K + 32) : 0;
   const size_t front = (x > red ? x : red) / 16 * 16 + 16;
   const int ses = sdt == SCALE_F32 ? 4 : 2;
@@ -394,26 +442,30 @@ size_t rows_lds_bytes(int wt, int sdt, int nblk, bool xl, int M, int K) {
 }
 
 // Can the row-partitioned kernel run this problem with P workgroups?  Sets
-// the row-block count and whether X is staged in LDS.
-bool rows_ok(const GemmArgs& a, int wt, int P, int* nblk_out, bool* xl_out, int xl_pref) {
-  if (a.M < 1 || a.M > 16 || !a.xvec || !a.wvec || a.K % 128 != 0 || P < 1) return false;
+// the row-block count, whether X is staged in LDS, and the number of 16-row
+// activation strips (1 up to 16 rows; 2 up to 32 rows with 3+ row blocks).
+bool rows_ok(const GemmArgs& a, int wt, int P, int* nblk_out, bool* xl_out, int* ms_out, int xl_pref) {
+  if (a.M < 1 || a.M > 32 || !a.xvec || !a.wvec || a.K % 128 != 0 || P < 1) return false;
   if (a.K / 128 < 8) return false;  // every wavefront of the K split (<= 8) gets at least one chunk
+  const int ms = a.M > 16 ? 2 : 1;
   const int rows = (a.N + P - 1) / P;
   const int nblk = (rows + 15) / 16;
-  if (nblk > kRowsMaxBlocks) return false;
+  if (nblk > kRowsMaxBlocks || (ms > 1 && nblk < 3)) return false;
   const int64_t rb = wt == W_INT4 ? a.ldw * 4 : a.ldw;
   if (static_cast<int64_t>(a.N) * rb >= (int64_t{1} << 31)) return false;
   if ((static_cast<int64_t>(a.M) * a.ldx + a.K) * 2 >= (int64_t{1} << 31)) return false;
-  bool xl = xl_pref != 0 && rows_lds_bytes(wt, a.sdt, nblk, true, a.M, a.K) <= kRowsMaxLds;
-  if (!xl && rows_lds_bytes(wt, a.sdt, nblk, false, a.M, a.K) > kRowsMaxLds) return false;
+  bool xl = ms == 1 && xl_pref != 0 && rows_lds_bytes(wt, a.sdt, nblk, true, a.M, a.K, ms) <= kRowsMaxLds;
+  if (!xl && rows_lds_bytes(wt, a.sdt, nblk, false, a.M, a.K, ms) > kRowsMaxLds) return false;
   *nblk_out = nblk;
   *xl_out = xl;
+  *ms_out = ms;
   return true;
 }
 
-hipError_t launch_rows(int wt, const GemmArgs& a, int nblk, bool xl, hipStream_t stream) {
-#define HSQ_RX(WT_, SDT_) \
-  return xl ? launch_rows_x<WT_, SDT_, true>(a, nblk, stream) : launch_rows_x<WT_, SDT_, false>(a, nblk, stream);
+hipError_t launch_rows(int wt, const GemmArgs& a, int nblk, bool xl, int ms, hipStream_t stream) {
+#define HSQ_RX(WT_, SDT_)                                                    \
+  return xl ? launch_rows_x<WT_, SDT_, true>(a, nblk, ms, stream)           \
+            : launch_rows_x<WT_, SDT_, false>(a, nblk, ms, stream);
   if (wt == W_INT4) {
     if (a.sdt == SCALE_BF16) HSQ_RX(W_INT4, SCALE_BF16)
     if (a.sdt == SCALE_F16) HSQ_RX(W_INT4, SCALE_F16)
