@@ -34,6 +34,12 @@ extern int rows_kw8;
 bool gemv_ok(const GemmArgs& a, int wt, int P, int kw_pref, int* kw_out, int* rows_max);
 hipError_t launch_gemv(int wt, const GemmArgs& a, int kw, hipStream_t stream);
 extern int gemv_rd;
+bool skinny_ok(const GemmArgs& a, int wt, int kc);
+hipError_t launch_skinny(int wt, const GemmArgs& a, int s, int nb, int kc, bool xd, hipStream_t stream);
+int skinny_slot_floats(int mt, int s, int nb);
+int skinny_bt(int s, int nb);
+int skinny_max_units(int s, int nb, int kc);
+bool skinny_fits(int wt, int m, int s, int nb, int kc, bool xd);
 hipError_t launch_int4_dequant(const uint32_t* packed, int64_t ldw, const void* scale, int64_t lds, int sdt,
                                const int32_t* zero, int64_t ldz, void* out, int64_t ldo, int odt, int N, int K,
                                int group, hipStream_t stream);
@@ -72,6 +78,10 @@ struct Tuning {
   int mid_nj = 0;          // its 32-column blocks per wave (0 = heuristic)
   int rows_ms2_off = 0;    // 1: the row-partitioned kernel only up to 16 rows
   int prefill_wg_per_cu = 0;
+  int skinny = 0;          // register-streamed decode kernel: 0 = where measured faster, 1 = always (M <= 64), 2 = never
+  int skinny_layout = -1;  // its (S, NB, KC) layout index (-1 = heuristic)
+  int skinny_wg = 0;       // its workgroups per CU (0 = 1)
+  int skinny_xd = -1;      // its largest M loading X fragments per wave (-1 = none)
 };
 
 int env_int(const char* name) {
@@ -107,6 +117,10 @@ const Tuning& tuning() {
     r.mid_nj = env_int("HS_MID_NJ");
     r.rows_ms2_off = env_int("HS_ROWS_MS2_OFF");
     r.prefill_wg_per_cu = env_int("HS_PREFILL_WG_PER_CU");
+    r.skinny = env_int("HS_SKINNY");
+    if (std::getenv("HS_SKINNY_LAYOUT") != nullptr) r.skinny_layout = env_int("HS_SKINNY_LAYOUT");
+    r.skinny_wg = env_int("HS_SKINNY_WG");
+    if (std::getenv("HS_SKINNY_XD") != nullptr) r.skinny_xd = env_int("HS_SKINNY_XD");
     return r;
   }();
   return t;
@@ -131,6 +145,8 @@ struct Plan {
   bool decode = true;
   bool wide = false;    // 256x256-tile prefill kernel
   bool mid = false;     // LDS-DMA streaming kernel, 32-row MFMA blocks
+  bool skinny = false;  // register-streamed decode kernel
+  int SS = 1, SNB = 2, SKC = 4;
   int BMI = 1, NJ = 1, NW = 4;
   int MT = 1, S = 1, BM = 256, NB = 1;
   int T = 0, TM = 1, G = 0;
@@ -145,12 +161,64 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 int stream_nb(int M) { return M <= 16 ? 8 : (M <= 32 ? 4 : 2); }
 
+// Register-streamed decode kernel layouts: S 16-row blocks per wave, NB
+// block groups, KC K phases (NB * KC = 8 wavefronts).
+struct SkinnyLayout {
+  int s, nb, kc;
+};
+constexpr SkinnyLayout kSkinnyLayouts[] = {{1, 2, 4}, {1, 4, 2}, {2, 2, 4}, {1, 8, 1}, {2, 4, 2}, {2, 1, 8}};
+constexpr int kSkinnyLayoutCount = 6;
+
+bool skinny_xd(int M) {
+  const Tuning& tn = tuning();
+  return M <= (tn.skinny_xd >= 0 ? tn.skinny_xd : 0);
+}
+
+SkinnyLayout skinny_layout(int wt, int M, int K) {
+  const Tuning& tn = tuning();
+  int i = tn.skinny_layout;
+  // Measured on MI355X (17408 -> 5120, 8192 -> 5120): two row blocks per
+  // wave over four K phases up to 16 rows (INT4), one 128-row tile over one
+  // phase above.
+  if (i < 0 || i >= kSkinnyLayoutCount) i = (wt == W_INT4 && M <= 16) ? 2 : 3;
+  const auto usable = [&](int j) {
+    const SkinnyLayout& l = kSkinnyLayouts[j];
+    return K % (128 * l.kc) == 0 && (l.s == 1 || M <= 32) && skinny_fits(wt, M, l.s, l.nb, l.kc, skinny_xd(M));
+  };
+  // Fall back to fewer K phases (or one row block per wave) when the layout
+  // does not divide K or does not fit LDS.
+  if (!usable(i)) i = 1;
+  if (!usable(i)) i = 3;
+  return kSkinnyLayouts[i];
+}
+
 // `fast`: the streaming kernel can run this problem (see stream_ok); `wide`:
 // the 256x256-tile prefill kernel can (see wide_ok).
-Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast, bool wide, bool mid) {
+Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast, bool wide, bool mid, bool skinny) {
   Plan p;
   const int cus = device_cus();
   const Tuning& tn = tuning();
+  if (skinny && M <= 64) {
+    p.skinny = true;
+    p.decode = false;
+    const SkinnyLayout l = skinny_layout(wt, M, K);
+    p.SS = l.s;
+    p.SNB = l.nb;
+    p.SKC = l.kc;
+    p.T = static_cast<int>(cdiv(N, skinny_bt(p.SS, p.SNB)));
+    p.G = K / (128 * p.SKC);
+    p.U = static_cast<int64_t>(p.T) * p.G;
+    int64_t wgs = static_cast<int64_t>(cus) * (tn.skinny_wg > 0 ? tn.skinny_wg : 1);
+    // Each workgroup stages the scales of all its units in LDS: at most
+    // skinny_max_units() of them.
+    const int64_t need = cdiv(p.U, skinny_max_units(p.SS, p.SNB, p.SKC));
+    wgs = wgs > need ? wgs : need;
+    p.P = static_cast<int>(p.U < wgs ? p.U : wgs);
+    p.slot_floats = skinny_slot_floats((M + 15) / 16, p.SS, p.SNB);
+    p.counter_bytes = kCounterBytes;
+    p.ws_bytes = p.counter_bytes + static_cast<int64_t>(p.P) * 2 * p.slot_floats * 4;
+    return p;
+  }
   if (mid && !tn.mid_off && M >= (tn.mid_min_m > 0 ? tn.mid_min_m : 17) && M <= 128) {
     p.mid = true;
     p.BMI = static_cast<int>(cdiv(M, 32));
@@ -241,7 +309,13 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   const Tuning& tn = tuning();
   // Decode with at most 16 activation rows: row-partitioned kernels, one
   // partition per workgroup, no workspace.  Block-major when X fits in LDS.
-  if (!tn.gemv_off && a.M <= 16) {
+  // The register-streamed kernel wins on narrow outputs (N <= K) from 5
+  // (INT4) / 9 (FP8) activation rows; the row-partitioned kernels below keep
+  // fewer rows and the wide outputs.
+  const bool skinny_auto = a.N <= a.K && a.M >= (wt == W_INT4 ? 5 : 9);
+  const bool use_skinny = tn.skinny != 2 && (tn.skinny == 1 || skinny_auto) && a.M <= 64 &&
+                          skinny_ok(a, wt, skinny_layout(wt, a.M, a.K).kc);
+  if (!use_skinny && !tn.gemv_off && a.M <= 16) {
     const int P = device_cus() * (tn.gemv_wg > 0 ? tn.gemv_wg : 1);
     int kw = 0, rows_max = 0;
     if (gemv_ok(a, wt, P, tn.gemv_kw > 0 ? tn.gemv_kw : 8, &kw, &rows_max)) {
@@ -251,7 +325,7 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
       return hip_code(launch_gemv(wt, a, kw, stream));
     }
   }
-  if (!tn.rows_off && a.M <= (tn.rows_ms2_off ? 16 : 32)) {
+  if (!use_skinny && !tn.rows_off && a.M <= (tn.rows_ms2_off ? 16 : 32)) {
     const int P = device_cus() * (tn.rows_wg > 0 ? tn.rows_wg : 1);
     int nblk = 0, ms = 1;
     bool xl = false;
@@ -267,7 +341,7 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   }
   const int nb = tn.st_nb > 0 ? tn.st_nb : stream_nb(a.M);
   const Plan p = make_plan(wt, a.M, a.N, a.K, decode_kfull(a.K, a.xvec, a.wvec), stream_ok(a, wt, nb),
-                           wide_ok(a, wt), mid_ok(a, wt));
+                           wide_ok(a, wt), mid_ok(a, wt), use_skinny);
   if (p.T > kMaxTiles) return HS_EUNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < p.ws_bytes) return HS_EWORKSPACE;
   a.G = p.G;
@@ -278,7 +352,8 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   a.P = p.P;
   a.counters = reinterpret_cast<int*>(workspace);
   a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.counter_bytes);
-  hipError_t e = p.mid      ? launch_mid(wt, a, p.BMI, p.NJ, p.NW, stream)
+  hipError_t e = p.skinny   ? launch_skinny(wt, a, p.SS, p.SNB, p.SKC, skinny_xd(a.M), stream)
+                 : p.mid    ? launch_mid(wt, a, p.BMI, p.NJ, p.NW, stream)
                  : p.stream ? launch_stream(wt, a, p.MT, p.S, stream)
                  : p.decode ? launch_decode(wt, a, p.MT, p.S, stream)
                  : p.wide   ? launch_wide(wt, a, stream)
@@ -312,10 +387,12 @@ int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
   for (int kfull = 0; kfull < 2; ++kfull)
     for (int fast = 0; fast < 2; ++fast)
       for (int wide = 0; wide < 2; ++wide)
-        for (int mid = 0; mid < 2; ++mid) {
-          const int64_t b = hsq::make_plan(kind, M, N, K, kfull != 0, fast != 0, wide != 0, mid != 0).ws_bytes;
-          best = b > best ? b : best;
-        }
+        for (int mid = 0; mid < 2; ++mid)
+          for (int sk = 0; sk < 2; ++sk) {
+            const int64_t b =
+                hsq::make_plan(kind, M, N, K, kfull != 0, fast != 0, wide != 0, mid != 0, sk != 0).ws_bytes;
+            best = b > best ? b : best;
+          }
   return best;
 }
 

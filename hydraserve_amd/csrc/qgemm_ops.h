@@ -27,6 +27,26 @@ __device__ __forceinline__ bf16x8_t int4_operand(uint32_t w, uint32_t nib_mask, 
   return __builtin_bit_cast(bf16x8_t, p);
 }
 
+// int4_operand of two words at once: each right shift is one 64-bit shift
+// of the pair (w1:w0).  The bits of w1 that the shift moves into the low
+// word land at bit 20 or above, outside the nibble mask of every position
+// they reach.
+__device__ __forceinline__ void int4_operand2(uint32_t w0, uint32_t w1, uint32_t nib_mask, uint32_t magic,
+                                              bf16x8_t& b0, bf16x8_t& b1) {
+  const uint64_t v = (static_cast<uint64_t>(w1) << 32) | w0;
+  u32x4_t p0, p1;
+  p0[0] = insert_nibbles(nib_mask, w0, magic);
+  p1[0] = insert_nibbles(nib_mask, w1, magic);
+#pragma unroll
+  for (int i = 1; i < 4; ++i) {
+    const uint64_t t = v >> (4 * i);
+    p0[i] = insert_nibbles(nib_mask, static_cast<uint32_t>(t), magic);
+    p1[i] = insert_nibbles(nib_mask, static_cast<uint32_t>(t >> 32), magic);
+  }
+  b0 = __builtin_bit_cast(bf16x8_t, p0);
+  b1 = __builtin_bit_cast(bf16x8_t, p1);
+}
+
 // bf16 (x0..x7) -> (x0, x4, x1, x5, x2, x6, x3, x7), matching int4_operand.
 __device__ __forceinline__ u32x4_t permute_x(u32x4_t d) {
   u32x4_t e;
