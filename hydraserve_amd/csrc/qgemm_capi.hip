@@ -309,10 +309,10 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   const Tuning& tn = tuning();
   // Decode with at most 16 activation rows: row-partitioned kernels, one
   // partition per workgroup, no workspace.  Block-major when X fits in LDS.
-  // The register-streamed kernel wins on narrow outputs (N <= K) from 5
+  // The register-streamed kernel wins on narrow outputs (N < K) from 5
   // (INT4) / 9 (FP8) activation rows; the row-partitioned kernels below keep
   // fewer rows and the wide outputs.
-  const bool skinny_auto = a.N <= a.K && a.M >= (wt == W_INT4 ? 5 : 9);
+  const bool skinny_auto = a.N < a.K && a.M >= (wt == W_INT4 ? 5 : 9);
   const bool use_skinny = tn.skinny != 2 && (tn.skinny == 1 || skinny_auto) && a.M <= 64 &&
                           skinny_ok(a, wt, skinny_layout(wt, a.M, a.K).kc);
   if (!use_skinny && !tn.gemv_off && a.M <= 16) {

@@ -78,12 +78,16 @@ struct Skinny {
   // start: INT4 one per (unit, phase, row), FP8 one per (unit, phase).
   static constexpr int SROW = WT == W_INT4 ? BT : 1;
   static constexpr int UMAX = kSkinnyMaxEntries / (BT * KC);
+  // Row-major [row][unit*KC + phase] with an odd row stride: the staging
+  // writes (consecutive lanes: consecutive groups of one row) and the
+  // per-unit reads (four rows, one group) both spread over the banks.
+  static constexpr int SPW = UMAX * KC + 1;
 
   struct Smem {
     __attribute__((aligned(16))) uint8_t x[XD ? 1 : 2][KC][XD ? 16 : MR * XROW];
     __attribute__((aligned(16))) f32x4_t red[KC > 1 ? KC - 1 : 1][NB][S][MT][64];
-    __attribute__((aligned(16))) float sc[UMAX][KC][SROW];                      // scales
-    __attribute__((aligned(16))) float nz[WT == W_INT4 ? UMAX : 1][KC][SROW];  // -(128 + zero point)
+    __attribute__((aligned(16))) float sc[SROW][SPW];                        // scales
+    __attribute__((aligned(16))) float nz[WT == W_INT4 ? SROW : 1][SPW];  // -(128 + zero point)
     int flag;
   };
 
@@ -192,10 +196,10 @@ __global__ __launch_bounds__(64 * NB * KC) void qgemm_skinny_kernel(GemmArgs a) 
             if constexpr (SDT == SCALE_F32) sf = __uint_as_float(sv[k]);
             else if constexpr (SDT == SCALE_BF16) sf = __uint_as_float(sv[k] << 16);
             else sf = __half2float(__ushort_as_half(static_cast<unsigned short>(sv[k])));
-            sm.sc[du][q][rl] = sf;
+            sm.sc[rl][du * KC + q] = sf;
             if constexpr (WT == W_INT4) {
               const int row = t * D::BT + rl;
-              sm.nz[du][q][rl] = -(128.0f + static_cast<float>((zv[k] >> (4 * (row & 7))) & 0xFu));
+              sm.nz[rl][du * KC + q] = -(128.0f + static_cast<float>((zv[k] >> (4 * (row & 7))) & 0xFu));
             }
           }
         }
@@ -437,13 +441,16 @@ __global__ __launch_bounds__(64 * NB * KC) void qgemm_skinny_kernel(GemmArgs a) 
       const int rl = (bg * S + s) * 16 + 4 * h;
       f32x4_t sc;
       if constexpr (WT == W_FP8) {
-        const float s0 = sm.sc[du][ph][0];
+        const float s0 = sm.sc[0][du * KC + ph];
         sc = f32x4_t{s0, s0, s0, s0};
       } else {
-        sc = *reinterpret_cast<const f32x4_t*>(&sm.sc[du][ph][rl]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[e] = sm.sc[rl + e][du * KC + ph];
       }
       if constexpr (WT == W_INT4) {
-        const f32x4_t nz = *reinterpret_cast<const f32x4_t*>(&sm.nz[du][ph][rl]);
+        f32x4_t nz;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) nz[e] = sm.nz[rl + e][du * KC + ph];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -499,7 +506,7 @@ bool skinny_fits(int wt, int m, int s, int nb, int kc, bool xd) {
   const size_t red = (kc > 1 ? kc - 1 : 1) * nb * s * mt * 1024;
   const size_t umax = kSkinnyMaxEntries / (bt * kc);
   const size_t srow = wt == W_INT4 ? bt : 1;
-  const size_t sc = (umax * kc * srow * 4 + 15) / 16 * 16;
+  const size_t sc = ((umax * kc + 1) * srow * 4 + 15) / 16 * 16;
   const size_t total = x + red + sc * (wt == W_INT4 ? 2 : 1) + 16;
   return total <= kSkinnyLdsLimit;
 }
