@@ -357,6 +357,33 @@ def sweep(torch, gen, dev):
     run("int4", "down", *DOWN, [1, 4, 16, 64, 512, 1024, 2048])
     run("fp8", "gate_up", *GATE_UP, [1, 16, 256, 2048])
     run("fp8", "down", *DOWN, [1, 16, 256, 2048])
+    # gate_up followed by SiLU-and-mul: fused epilogue on the interleaved
+    # weight vs the reference's sequence (GEMM, chunk, activation launch).
+    from hydraserve_amd.kernels import awq_gate_up_silu_mul, interleave_gate_up, silu_and_mul
+
+    per_copy = int4_bytes(*GATE_UP)
+    ws = make_int4(torch, *GATE_UP, copies_for(per_copy), gen, dev)
+    wis = [interleave_gate_up(w) for w in ws]
+    for m in (16, 64, 128):
+        x = torch.randn(m, GATE_UP[1], generator=gen, device=dev).to(torch.bfloat16)
+
+        def unfused(i):
+            import hydraserve_amd as hs
+
+            gate, up = hs.awq_linear(x, ws[i % len(ws)]).chunk(2, dim=-1)
+            return silu_and_mul(gate.contiguous(), up.contiguous())
+
+        def fused(i):
+            return awq_gate_up_silu_mul(x, wis[i % len(wis)])
+
+        ms_u, _ = graph_time_ms(torch, unfused, 10, len(ws))
+        ms_f, _ = graph_time_ms(torch, fused, 10, len(ws))
+        r = {"kind": "int4", "shape": "gate_up+silu_and_mul", "M": m, "N": GATE_UP[0], "K": GATE_UP[1],
+             "unfused_us": round(ms_u * 1e3, 2), "fused_us": round(ms_f * 1e3, 2)}
+        print(json.dumps(r), file=sys.stderr, flush=True)
+        out.append(r)
+    del ws, wis
+    torch.cuda.empty_cache()
     run("int4", "qkv", *QKV, [64, 1024])
     run("int4", "o_proj", *O_PROJ, [64, 1024])
     run("int4", "gdn_in", *GDN_IN, [64, 1024])

@@ -19,6 +19,7 @@ HS_KIND_FP8 = 1
 HS_DT_BF16 = 0
 HS_DT_F16 = 1
 HS_DT_F32 = 2
+HS_EUNSUPPORTED = 3
 
 # (name, restype, argtypes) for every symbol the header declares.
 _I64 = ctypes.c_int64
@@ -29,6 +30,7 @@ SIGNATURES = {
     "hs_error_string": (ctypes.c_char_p, [_I]),
     "hs_gemm_workspace_bytes": (_I64, [_I, _I, _I, _I]),
     "hs_int4_gemm": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _I64, _P]),
+    "hs_int4_gemm_silu_mul": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _I64, _P]),
     "hs_fp8_gemm": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _I, _I, _I, _P, _I64, _P]),
     "hs_int4_dequant": (_I, [_P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
     "hs_fp8_dequant": (_I, [_P, _I64, _P, _I64, _I, _P, _I64, _I, _I, _I, _P]),
@@ -133,6 +135,32 @@ def int4_gemm(x, packed, scale, zero_point, n: int, k: int, group: int):
         ),
         "hs_int4_gemm",
     )
+    return y
+
+
+def int4_gemm_silu_mul(x, packed, scale, zero_point, n: int, k: int, group: int):
+    """silu(gate) * up [M, N/2] (bf16) on a gate/up-interleaved weight of N rows,
+    or None where the fused kernel does not apply (HS_EUNSUPPORTED)."""
+    import torch
+
+    m = x.shape[0]
+    y = torch.empty(m, n // 2, device=x.device, dtype=x.dtype)
+    if m == 0 or n == 0:
+        return y
+    L = lib()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    need = L.hs_gemm_workspace_bytes(HS_KIND_INT4, m, n, k)
+    ws = workspaces.get(x.device, stream, need)
+    rc = L.hs_int4_gemm_silu_mul(
+        x.data_ptr(), x.stride(0), packed.data_ptr(), packed.stride(0),
+        scale.data_ptr(), scale.stride(0), dtype_code(scale.dtype),
+        zero_point.data_ptr(), zero_point.stride(0),
+        y.data_ptr(), y.stride(0), m, n, k, group,
+        ws.data_ptr(), ws.numel(), stream,
+    )
+    if rc == HS_EUNSUPPORTED:
+        return None
+    check(rc, "hs_int4_gemm_silu_mul")
     return y
 
 

@@ -427,6 +427,55 @@ int hs_int4_gemm(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_p
   return hsq::run_gemm(hsq::W_INT4, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
+int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,
+                          int64_t ld_scale, int scale_dtype, const int32_t* zero_point, int64_t ld_zero, void* y,
+                          int64_t ldy, int M, int N, int K, int group, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
+  if (M < 0 || N < 0 || K < 0) return HS_EINVAL;
+  if (group != 128) return HS_EUNSUPPORTED;
+  if (N % 32 != 0) return HS_EINVAL;
+  if (M == 0 || N == 0) return HS_OK;
+  if (K == 0) return HS_EUNSUPPORTED;
+  const int64_t kw = (K + 7) / 8, groups = (K + 127) / 128;
+  if (!x || !packed || !scale || !zero_point || !y) return HS_EINVAL;
+  if (ldx < K || ld_packed < kw || ld_scale < groups || ld_zero < groups || ldy < N / 2) return HS_EINVAL;
+  if (!hsq::valid_dt(scale_dtype)) return HS_EINVAL;
+  hsq::GemmArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.w = packed;
+  a.ldw = ld_packed;
+  a.scale = scale;
+  a.lds = ld_scale;
+  a.sdt = scale_dtype;
+  a.zero = zero_point;
+  a.ldz = ld_zero;
+  a.y = static_cast<uint16_t*>(y);
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.xvec = hsq::aligned16(x) && (ldx % 8 == 0);
+  a.wvec = hsq::aligned16(packed) && (ld_packed % 4 == 0);
+  a.tune = hsq::tuning().tune;
+  a.silu_mul = 1;
+  // Only the 17..128-row LDS-DMA kernel carries the fused epilogue.
+  if (M < 17 || M > 128 || !hsq::mid_ok(a, hsq::W_INT4)) return HS_EUNSUPPORTED;
+  const hsq::Plan p = hsq::make_plan(hsq::W_INT4, M, N, K, false, false, false, true, false);
+  if (!p.mid) return HS_EUNSUPPORTED;
+  if (p.T > hsq::kMaxTiles) return HS_EUNSUPPORTED;
+  if (workspace == nullptr || workspace_bytes < p.ws_bytes) return HS_EWORKSPACE;
+  a.G = p.G;
+  a.NB = p.NB;
+  a.T = p.T;
+  a.TM = p.TM;
+  a.U = p.U;
+  a.P = p.P;
+  a.counters = reinterpret_cast<int*>(workspace);
+  a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.counter_bytes);
+  return hsq::hip_code(hsq::launch_mid(hsq::W_INT4, a, p.BMI, p.NJ, p.NW, static_cast<hipStream_t>(stream)));
+}
+
 int hs_fp8_gemm(const void* x, int64_t ldx, const uint8_t* data, int64_t ld_data, const void* scale_inv,
                 int64_t ld_scale, int scale_dtype, void* y, int64_t ldy, int M, int N, int K, void* workspace,
                 int64_t workspace_bytes, void* stream) {

@@ -54,6 +54,8 @@ struct GemmArgs {
   int xvec;           // X base and row stride allow 16-byte loads
   int wvec;           // W base and row stride allow 16-byte loads
   int tune;           // kernel-specific experiment bits (0 = defaults)
+  int silu_mul;       // 1: W rows interleave gate and up in 16-row blocks and
+                      // y [M, N/2] receives silu(gate) * up (17..128-row kernel)
 };
 
 template <int SDT>

@@ -228,10 +228,40 @@ struct Mid {
     return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(&sm.ring[0][0] + slot + aoff + 4096 * i));
   }
 
+  // Fused SiLU-and-mul epilogue (a.silu_mul): weight rows interleave gate and
+  // up in 16-row blocks, so lanes l32 < 16 of a 32-column block hold gate
+  // row g = 16*(n/32) + l32 and lanes l32 + 16 the matching up row.  As in
+  // the reference's unfused sequence (hydraserve/model/runtime.py:1202-1210,
+  // silu_and_mul at hydraserve/kernels/activation.py:66-76), gate and up are
+  // rounded to bf16 first, then out = gate * sigmoid(gate) * up in fp32,
+  // rounded to bf16, into y [M, N/2].  N is a multiple of 32, so a lane and
+  // its partner are in range together.
+  static __device__ __forceinline__ void store_silu_mul(const GemmArgs& a, const f32x16_t& v, int n, int i,
+                                                        int l32, int h) {
+    const int col = (n >> 5) * 16 + (n & 15);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float own = bf16_to_f32(to_bf16_bits(v[e]));
+      const float up = __shfl_xor(own, 16);
+      const int m = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (l32 < 16 && m < a.M && n < a.N) {
+        const float sig = 1.0f / (1.0f + __expf(-own));
+        a.y[m * a.ldy + col] = to_bf16_bits(own * sig * up);
+      }
+    }
+  }
+
   // Lane (l32, h), register e of block (i, j): row 32i + 8(e/4) + 4h + e%4,
   // column t*BN + 32*NJ*wave + 32j + l32.
   static __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&acc)[BMI][NJ], int t,
                                                     int wave, int l32, int h) {
+    if (a.silu_mul) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < BMI; ++i) store_silu_mul(a, acc[i][j], t * BN + wave * 32 * NJ + 32 * j + l32, i, l32, h);
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int n = t * BN + wave * 32 * NJ + 32 * j + l32;
@@ -302,16 +332,23 @@ struct Mid {
 #pragma unroll
             for (int c = 0; c < 4; ++c) sum[i][j][4 * v + c] += x[i][j][v][c];
     }
+    if (a.silu_mul) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int n = t * BN + wave * 32 * NJ + 32 * j + l32;
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int i = 0; i < BMI; ++i)
+        for (int i = 0; i < BMI; ++i) store_silu_mul(a, sum[i][j], t * BN + wave * 32 * NJ + 32 * j + l32, i, l32, h);
+    } else {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-          if (m < a.M && n < a.N) a.y[m * a.ldy + n] = to_bf16_bits(sum[i][j][e]);
-        }
+      for (int j = 0; j < NJ; ++j) {
+        const int n = t * BN + wave * 32 * NJ + 32 * j + l32;
+#pragma unroll
+        for (int i = 0; i < BMI; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int m = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (m < a.M && n < a.N) a.y[m * a.ldy + n] = to_bf16_bits(sum[i][j][e]);
+          }
+      }
     }
     reset_counter(a.counters, t);
   }

@@ -2,5 +2,15 @@
 
 from .awq import awq_linear, dequantize_int4_weight
 from .fp8 import dequantize_fp8_weight, fp8_linear
+from .mlp import awq_gate_up_silu_mul, deinterleave_gate_up, interleave_gate_up, silu_and_mul
 
-__all__ = ["awq_linear", "dequantize_int4_weight", "fp8_linear", "dequantize_fp8_weight"]
+__all__ = [
+    "awq_linear",
+    "dequantize_int4_weight",
+    "fp8_linear",
+    "dequantize_fp8_weight",
+    "interleave_gate_up",
+    "deinterleave_gate_up",
+    "silu_and_mul",
+    "awq_gate_up_silu_mul",
+]

@@ -71,6 +71,27 @@ int hs_int4_gemm(const void* x, int64_t ldx,
                  void* workspace, int64_t workspace_bytes,
                  void* stream);
 
+/* The MLP's gate_up projection with SiLU-and-mul fused into the GEMM's store:
+ * out[M, N/2] = silu(gate) * up, gate and up being the bf16 outputs of
+ * hs_int4_gemm on W.  Replaces the gate_up _linear call, the chunk and the
+ * silu_and_mul launch of hydraserve/model/runtime.py:1202-1210
+ * (silu_and_mul: hydraserve/kernels/activation.py:4-25, kernel :66-76).
+ * W's rows interleave the gate and up halves in 16-row blocks (gate rows
+ * 16j..16j+15, then up rows 16j..16j+15: the load-time layout
+ * hydraserve_amd.kernels.mlp.interleave_gate_up builds).  N (both halves) a
+ * multiple of 32, ldy >= N/2; workspace as for hs_int4_gemm.  Returns
+ * HS_EUNSUPPORTED outside 17 <= M <= 128 or when K or the strides do not
+ * suit the kernel; the caller then runs hs_int4_gemm and the activation
+ * separately. */
+int hs_int4_gemm_silu_mul(const void* x, int64_t ldx,
+                          const int32_t* packed, int64_t ld_packed,
+                          const void* scale, int64_t ld_scale, int scale_dtype,
+                          const int32_t* zero_point, int64_t ld_zero,
+                          void* y, int64_t ldy,
+                          int M, int N, int K, int group,
+                          void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
 /* Y[M,N] = X[M,K] . (decode(W) * scale_inv[n/128, k/128])^T, fp32 accumulation,
  * bf16 output.  Replaces the GPU branch of fp8_linear
  * (hydraserve/kernels/fp8.py:24-97, Triton kernel fp8.py:104-168). */
