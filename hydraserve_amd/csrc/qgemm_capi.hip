@@ -459,8 +459,20 @@ int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int
   a.wvec = hsq::aligned16(packed) && (ld_packed % 4 == 0);
   a.tune = hsq::tuning().tune;
   a.silu_mul = 1;
-  // Only the 17..128-row LDS-DMA kernel carries the fused epilogue.
-  if (M < 17 || M > 128 || !hsq::mid_ok(a, hsq::W_INT4)) return HS_EUNSUPPORTED;
+  // The fused epilogue is in the block-major GEMV kernel (1..16 rows, X in
+  // LDS) and in the 17..128-row LDS-DMA kernel.
+  if (M <= 16) {
+    const hsq::Tuning& tn = hsq::tuning();
+    const int P = hsq::device_cus() * (tn.gemv_wg > 0 ? tn.gemv_wg : 1);
+    int kw = 0, rows_max = 0;
+    if (tn.gemv_off || !hsq::gemv_ok(a, hsq::W_INT4, P, tn.gemv_kw > 0 ? tn.gemv_kw : 8, &kw, &rows_max))
+      return HS_EUNSUPPORTED;
+    a.P = P;
+    a.T = K / 128;
+    a.G = rows_max;
+    return hsq::hip_code(hsq::launch_gemv(hsq::W_INT4, a, kw, static_cast<hipStream_t>(stream)));
+  }
+  if (M > 128 || !hsq::mid_ok(a, hsq::W_INT4)) return HS_EUNSUPPORTED;
   const hsq::Plan p = hsq::make_plan(hsq::W_INT4, M, N, K, false, false, false, true, false);
   if (!p.mid) return HS_EUNSUPPORTED;
   if (p.T > hsq::kMaxTiles) return HS_EUNSUPPORTED;

@@ -78,6 +78,25 @@ __host__ __device__ inline GemvLds gemv_lds(int wt, int sdt, int kw, int M, int 
   return l;
 }
 
+// Rows [*r0, *r1) of workgroup p: an even split of the N rows, or with the
+// fused SiLU-and-mul epilogue (a.silu_mul, N a multiple of 32) an even split
+// of the N/32 gate/up block pairs, so that both blocks of a pair land in one
+// workgroup.
+__host__ __device__ inline void gemv_partition(const GemmArgs& a, int p, int* r0, int* r1) {
+  if (a.silu_mul) {
+    const int64_t np = a.N / 32;
+    *r0 = 32 * static_cast<int>(p * np / a.P);
+    *r1 = 32 * static_cast<int>((p + 1) * np / a.P);
+  } else {
+    *r0 = static_cast<int>(static_cast<int64_t>(p) * a.N / a.P);
+    *r1 = static_cast<int>(static_cast<int64_t>(p + 1) * a.N / a.P);
+  }
+}
+
+__host__ __device__ inline int gemv_rows_max(const GemmArgs& a, int P) {
+  return a.silu_mul ? 32 * static_cast<int>((a.N / 32 + P - 1) / P) : (a.N + P - 1) / P;
+}
+
 // a.P = workgroups (row partitions); a.T = chunks per row (K / 128); a.G =
 // the largest partition (rows), which sized the LDS layout.
 template <int WT, int SDT, int KW, int RD>
@@ -90,8 +109,8 @@ __global__ __launch_bounds__(64 * KW) void qgemm_gemv_kernel(GemmArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(tid >> 6));
   const int lane = tid & 63, l16 = lane & 15, h = lane >> 4;
   const int p = blockIdx.x;
-  const int r0 = static_cast<int>(static_cast<int64_t>(p) * a.N / a.P);
-  const int r1 = static_cast<int>(static_cast<int64_t>(p + 1) * a.N / a.P);
+  int r0, r1;
+  gemv_partition(a, p, &r0, &r1);
   if (r0 >= r1) return;
   const int nr = r1 - r0;
   const int nblk = (nr + 15) / 16;
@@ -305,6 +324,40 @@ __global__ __launch_bounds__(64 * KW) void qgemm_gemv_kernel(GemmArgs a) {
 
   // ---- sum the KW partials of every block in wavefront order, store bf16 ------
   __syncthreads();
+  if (a.silu_mul) {
+    // Fused SiLU-and-mul: local blocks 2q (gate rows) and 2q+1 (the matching
+    // up rows) of the interleaved weight; r0 and nr are multiples of 32.  As
+    // in the reference's unfused sequence (hydraserve/model/runtime.py:
+    // 1202-1210, silu_and_mul at hydraserve/kernels/activation.py:66-76),
+    // gate and up are rounded to bf16 first, then out = gate * sigmoid(gate)
+    // * up in fp32, rounded to bf16, into y [M, N/2].
+    for (int q = wave; 2 * q < nblk; q += KW) {
+      f32x4_t g = *reinterpret_cast<const f32x4_t*>(red + ((0 * nblk + 2 * q) * 64 + lane) * 4);
+      f32x4_t u = *reinterpret_cast<const f32x4_t*>(red + ((0 * nblk + 2 * q + 1) * 64 + lane) * 4);
+#pragma unroll
+      for (int w = 1; w < KW; ++w) {
+        const f32x4_t vg = *reinterpret_cast<const f32x4_t*>(red + ((w * nblk + 2 * q) * 64 + lane) * 4);
+        const f32x4_t vu = *reinterpret_cast<const f32x4_t*>(red + ((w * nblk + 2 * q + 1) * 64 + lane) * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          g[e] += vg[e];
+          u[e] += vu[e];
+        }
+      }
+      const int col = r0 / 2 + 16 * q + l16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = 4 * h + e;
+        if (m < M) {
+          const float gb = bf16_to_f32(to_bf16_bits(g[e]));
+          const float ub = bf16_to_f32(to_bf16_bits(u[e]));
+          const float sig = 1.0f / (1.0f + __expf(-gb));
+          a.y[m * a.ldy + col] = to_bf16_bits(gb * sig * ub);
+        }
+      }
+    }
+    return;
+  }
   for (int b = wave; b < nblk; b += KW) {
     f32x4_t s = *reinterpret_cast<const f32x4_t*>(red + ((0 * nblk + b) * 64 + lane) * 4);
 #pragma unroll
@@ -357,7 +410,8 @@ bool gemv_ok(const GemmArgs& a, int wt, int P, int kw_pref, int* kw_out, int* ro
   if ((static_cast<int64_t>(a.M) * a.ldx + a.K) * 2 >= (int64_t{1} << 31)) return false;
   // Only with kw_pref wavefronts: fewer leave too few loads in flight (a
   // layout that does not fit goes to the row-partitioned kernel instead).
-  const int nr_max = (a.N + P - 1) / P;
+  if (a.silu_mul && (wt != W_INT4 || a.N % 32 != 0)) return false;
+  const int nr_max = gemv_rows_max(a, P);
   const int kw = kw_pref;
   if (a.K / 128 < kw) return false;  // every wavefront gets at least one chunk
   if (gemv_lds(wt, a.sdt, kw, a.M, a.K, nr_max).total > kGemvMaxLds) return false;

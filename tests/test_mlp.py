@@ -3,7 +3,8 @@
 CPU: the load-time interleave is a lossless row permutation (checked through
 the oracle's unpack and dequantizer, and by its inverse), and the fused C
 entry point validates its arguments like hs_int4_gemm.
-GPU: hs_int4_gemm_silu_mul (17..128 rows) and the unfused fallback against
+GPU: hs_int4_gemm_silu_mul (1..16 rows in the block-major GEMV kernel,
+17..128 rows in the LDS-DMA streaming kernel) and the unfused fallback against
 the oracle, with the bars of tests/test_gemm_gpu.py applied to
 silu(bf16(gate)) * bf16(up) computed from the float64 oracle GEMM, and
 against the product path's own unfused sequence (awq_linear on the original
@@ -82,7 +83,7 @@ def test_fused_entry_point_validates_arguments():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m", [1, 8, 17, 32, 64, 100, 128, 130])
+@pytest.mark.parametrize("m", [1, 4, 8, 16, 17, 32, 64, 100, 128, 130])
 @pytest.mark.parametrize("n,k", [(2048, 1024), (1536, 640)])
 def test_fused_gate_up_silu_mul(m, n, k):
     if not torch.cuda.is_available():
