@@ -465,12 +465,21 @@ int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int
     const hsq::Tuning& tn = hsq::tuning();
     const int P = hsq::device_cus() * (tn.gemv_wg > 0 ? tn.gemv_wg : 1);
     int kw = 0, rows_max = 0;
-    if (tn.gemv_off || !hsq::gemv_ok(a, hsq::W_INT4, P, tn.gemv_kw > 0 ? tn.gemv_kw : 8, &kw, &rows_max))
-      return HS_EUNSUPPORTED;
-    a.P = P;
+    if (!tn.gemv_off && hsq::gemv_ok(a, hsq::W_INT4, P, tn.gemv_kw > 0 ? tn.gemv_kw : 8, &kw, &rows_max)) {
+      a.P = P;
+      a.T = K / 128;
+      a.G = rows_max;
+      return hsq::hip_code(hsq::launch_gemv(hsq::W_INT4, a, kw, static_cast<hipStream_t>(stream)));
+    }
+    // X too large for the block-major kernel's LDS: the row-partitioned
+    // kernel (X in LDS when it fits, else A fragments from global memory).
+    const int Pr = hsq::device_cus() * (tn.rows_wg > 0 ? tn.rows_wg : 1);
+    int nblk = 0, ms = 1;
+    bool xl = false;
+    if (tn.rows_off || !hsq::rows_ok(a, hsq::W_INT4, Pr, &nblk, &xl, &ms, tn.rows_xl)) return HS_EUNSUPPORTED;
+    a.P = Pr;
     a.T = K / 128;
-    a.G = rows_max;
-    return hsq::hip_code(hsq::launch_gemv(hsq::W_INT4, a, kw, static_cast<hipStream_t>(stream)));
+    return hsq::hip_code(hsq::launch_rows(hsq::W_INT4, a, nblk, xl, ms, static_cast<hipStream_t>(stream)));
   }
   if (M > 128 || !hsq::mid_ok(a, hsq::W_INT4)) return HS_EUNSUPPORTED;
   const hsq::Plan p = hsq::make_plan(hsq::W_INT4, M, N, K, false, false, false, true, false);

@@ -55,8 +55,28 @@ struct GemmArgs {
   int wvec;           // W base and row stride allow 16-byte loads
   int tune;           // kernel-specific experiment bits (0 = defaults)
   int silu_mul;       // 1: W rows interleave gate and up in 16-row blocks and
-                      // y [M, N/2] receives silu(gate) * up (17..128-row kernel)
+                      // y [M, N/2] receives silu(gate) * up
 };
+
+// Row partitions of the row-partitioned decode kernels: rows [*r0, *r1) of
+// workgroup p of a.P.  An even split of the N rows, or with the fused
+// SiLU-and-mul epilogue (a.silu_mul, N a multiple of 32) an even split of the
+// N/32 gate/up block pairs, so both blocks of a pair land in one workgroup.
+__host__ __device__ inline void row_partition(const GemmArgs& a, int p, int* r0, int* r1) {
+  if (a.silu_mul) {
+    const int64_t np = a.N / 32;
+    *r0 = 32 * static_cast<int>(p * np / a.P);
+    *r1 = 32 * static_cast<int>((p + 1) * np / a.P);
+  } else {
+    *r0 = static_cast<int>(static_cast<int64_t>(p) * a.N / a.P);
+    *r1 = static_cast<int>(static_cast<int64_t>(p + 1) * a.N / a.P);
+  }
+}
+
+// The largest partition row_partition gives with P workgroups.
+__host__ __device__ inline int row_partition_max(const GemmArgs& a, int P) {
+  return a.silu_mul ? 32 * static_cast<int>((a.N / 32 + P - 1) / P) : (a.N + P - 1) / P;
+}
 
 template <int SDT>
 __device__ __forceinline__ float load_scale(const void* p, int64_t idx) {

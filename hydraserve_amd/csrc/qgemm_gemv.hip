@@ -78,25 +78,6 @@ __host__ __device__ inline GemvLds gemv_lds(int wt, int sdt, int kw, int M, int 
   return l;
 }
 
-// Rows [*r0, *r1) of workgroup p: an even split of the N rows, or with the
-// fused SiLU-and-mul epilogue (a.silu_mul, N a multiple of 32) an even split
-// of the N/32 gate/up block pairs, so that both blocks of a pair land in one
-// workgroup.
-__host__ __device__ inline void gemv_partition(const GemmArgs& a, int p, int* r0, int* r1) {
-  if (a.silu_mul) {
-    const int64_t np = a.N / 32;
-    *r0 = 32 * static_cast<int>(p * np / a.P);
-    *r1 = 32 * static_cast<int>((p + 1) * np / a.P);
-  } else {
-    *r0 = static_cast<int>(static_cast<int64_t>(p) * a.N / a.P);
-    *r1 = static_cast<int>(static_cast<int64_t>(p + 1) * a.N / a.P);
-  }
-}
-
-__host__ __device__ inline int gemv_rows_max(const GemmArgs& a, int P) {
-  return a.silu_mul ? 32 * static_cast<int>((a.N / 32 + P - 1) / P) : (a.N + P - 1) / P;
-}
-
 // a.P = workgroups (row partitions); a.T = chunks per row (K / 128); a.G =
 // the largest partition (rows), which sized the LDS layout.
 template <int WT, int SDT, int KW, int RD>
@@ -110,7 +91,7 @@ __global__ __launch_bounds__(64 * KW) void qgemm_gemv_kernel(GemmArgs a) {
   const int lane = tid & 63, l16 = lane & 15, h = lane >> 4;
   const int p = blockIdx.x;
   int r0, r1;
-  gemv_partition(a, p, &r0, &r1);
+  row_partition(a, p, &r0, &r1);
   if (r0 >= r1) return;
   const int nr = r1 - r0;
   const int nblk = (nr + 15) / 16;
@@ -411,7 +392,7 @@ bool gemv_ok(const GemmArgs& a, int wt, int P, int kw_pref, int* kw_out, int* ro
   // Only with kw_pref wavefronts: fewer leave too few loads in flight (a
   // layout that does not fit goes to the row-partitioned kernel instead).
   if (a.silu_mul && (wt != W_INT4 || a.N % 32 != 0)) return false;
-  const int nr_max = gemv_rows_max(a, P);
+  const int nr_max = row_partition_max(a, P);
   const int kw = kw_pref;
   if (a.K / 128 < kw) return false;  // every wavefront gets at least one chunk
   if (gemv_lds(wt, a.sdt, kw, a.M, a.K, nr_max).total > kGemvMaxLds) return false;

@@ -94,8 +94,8 @@ __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(tid >> 6));
   const int lane = tid & 63, l16 = lane & 15, h = lane >> 4;
   const int p = blockIdx.x;
-  const int r0 = static_cast<int>(static_cast<int64_t>(p) * a.N / a.P);
-  const int r1 = static_cast<int>(static_cast<int64_t>(p + 1) * a.N / a.P);
+  int r0, r1;
+  row_partition(a, p, &r0, &r1);
   if (r0 >= r1) return;
   const int nr = r1 - r0;
 
@@ -336,6 +336,43 @@ __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
     for (int s = 0; s < MS; ++s)
       *reinterpret_cast<f32x4_t*>(red + (((wave * NBLK + b) * MS + s) * 64 + lane) * 4) = acc[b][s];
   __syncthreads();
+  if (a.silu_mul) {
+    // Fused SiLU-and-mul: local blocks 2q (gate rows) and 2q+1 (the matching
+    // up rows) of the interleaved weight; r0 and nr are multiples of 32.  As
+    // in the reference's unfused sequence (hydraserve/model/runtime.py:
+    // 1202-1210, silu_and_mul at hydraserve/kernels/activation.py:66-76),
+    // gate and up are rounded to bf16 first, then out = gate * sigmoid(gate)
+    // * up in fp32, rounded to bf16, into y [M, N/2].
+    for (int i = wave; i < (NBLK / 2) * MS; i += KW) {
+      const int q = i / MS, s = i - q * MS;
+      if (32 * q >= nr) continue;
+      const int ig = (2 * q) * MS + s, iu = (2 * q + 1) * MS + s;
+      f32x4_t g = *reinterpret_cast<const f32x4_t*>(red + (ig * 64 + lane) * 4);
+      f32x4_t u = *reinterpret_cast<const f32x4_t*>(red + (iu * 64 + lane) * 4);
+#pragma unroll
+      for (int w = 1; w < KW; ++w) {
+        const f32x4_t vg = *reinterpret_cast<const f32x4_t*>(red + ((w * NBLK * MS + ig) * 64 + lane) * 4);
+        const f32x4_t vu = *reinterpret_cast<const f32x4_t*>(red + ((w * NBLK * MS + iu) * 64 + lane) * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          g[e] += vg[e];
+          u[e] += vu[e];
+        }
+      }
+      const int col = r0 / 2 + 16 * q + l16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = 16 * s + 4 * h + e;
+        if (m < a.M) {
+          const float gb = bf16_to_f32(to_bf16_bits(g[e]));
+          const float ub = bf16_to_f32(to_bf16_bits(u[e]));
+          const float sig = 1.0f / (1.0f + __expf(-gb));
+          a.y[m * a.ldy + col] = to_bf16_bits(gb * sig * ub);
+        }
+      }
+    }
+    return;
+  }
   for (int i = wave; i < NBLK * MS; i += KW) {
     const int b = i / MS, s = i - b * MS;
     f32x4_t sum = *reinterpret_cast<const f32x4_t*>(red + (i * 64 + lane) * 4);
@@ -408,11 +445,11 @@ static hipError_t launch_rows_x(const GemmArgs& a, int nblk, int ms, hipStream_t
   if (ms != 1) return hipErrorInvalidValue;
   if constexpr (WT == W_INT4 && XL) {
     HSQ_RW(1, 8, 4) HSQ_RW(2, 8, 4) HSQ_RW(3, 4, 4) HSQ_RW(4, 4, 4) HSQ_RW(5, 4, 2) HSQ_RW(6, 4, 2)
-    HSQ_RW(7, 4, 2) HSQ_RW(8, 4, 2) HSQ_RW(9, 4, 2)
+    HSQ_RW(7, 4, 2) HSQ_RW(8, 4, 2) HSQ_RW(9, 4, 2) HSQ_RW(10, 4, 2)
     HSQ_RW(5, 8, 1) HSQ_RW(6, 8, 1) HSQ_RW(7, 8, 1) HSQ_RW(8, 8, 1) HSQ_RW(9, 8, 1)
   } else if constexpr (WT == W_INT4) {
     HSQ_RW(1, 8, 4) HSQ_RW(2, 8, 4) HSQ_RW(3, 4, 2) HSQ_RW(4, 4, 2) HSQ_RW(5, 4, 1) HSQ_RW(6, 4, 1)
-    HSQ_RW(7, 4, 1) HSQ_RW(8, 4, 1) HSQ_RW(9, 4, 1)
+    HSQ_RW(7, 4, 1) HSQ_RW(8, 4, 1) HSQ_RW(9, 4, 1) HSQ_RW(10, 4, 1)
     HSQ_RW(5, 8, 1) HSQ_RW(6, 8, 1) HSQ_RW(7, 8, 1) HSQ_RW(8, 8, 1) HSQ_RW(9, 8, 1)
   } else if constexpr (XL) {
     HSQ_RW(1, 8, 4) HSQ_RW(2, 8, 4) HSQ_RW(3, 4, 2) HSQ_RW(4, 4, 2) HSQ_RW(5, 4, 1) HSQ_RW(6, 4, 1)
@@ -427,6 +464,7 @@ static hipError_t launch_rows_x(const GemmArgs& a, int nblk, int ms, hipStream_t
 #undef HSQ_RW2
 
 constexpr int kRowsMaxBlocks = 9;
+constexpr int kRowsMaxBlocksSilu = 10;  // INT4 only: whole gate/up pairs per workgroup
 constexpr size_t kRowsMaxLds = 160 * 1024;
 
 size_t rows_lds_bytes(int wt, int sdt, int nblk, bool xl, int M, int K, int ms) {
@@ -448,9 +486,10 @@ bool rows_ok(const GemmArgs& a, int wt, int P, int* nblk_out, bool* xl_out, int*
   if (a.M < 1 || a.M > 32 || !a.xvec || !a.wvec || a.K % 128 != 0 || P < 1) return false;
   if (a.K / 128 < 8) return false;  // every wavefront of the K split (<= 8) gets at least one chunk
   const int ms = a.M > 16 ? 2 : 1;
-  const int rows = (a.N + P - 1) / P;
+  if (a.silu_mul && (wt != W_INT4 || a.N % 32 != 0 || ms > 1)) return false;
+  const int rows = row_partition_max(a, P);
   const int nblk = (rows + 15) / 16;
-  if (nblk > kRowsMaxBlocks || (ms > 1 && nblk < 3)) return false;
+  if (nblk > (a.silu_mul ? kRowsMaxBlocksSilu : kRowsMaxBlocks) || (ms > 1 && nblk < 3)) return false;
   const int64_t rb = wt == W_INT4 ? a.ldw * 4 : a.ldw;
   if (static_cast<int64_t>(a.N) * rb >= (int64_t{1} << 31)) return false;
   if ((static_cast<int64_t>(a.M) * a.ldx + a.K) * 2 >= (int64_t{1} << 31)) return false;
