@@ -364,7 +364,7 @@ def sweep(torch, gen, dev):
     per_copy = int4_bytes(*GATE_UP)
     ws = make_int4(torch, *GATE_UP, copies_for(per_copy), gen, dev)
     wis = [interleave_gate_up(w) for w in ws]
-    for m in (1, 4, 16, 64, 128):
+    for m in (1, 4, 16, 64, 128, 2048):
         x = torch.randn(m, GATE_UP[1], generator=gen, device=dev).to(torch.bfloat16)
 
         def unfused(i):

@@ -487,7 +487,23 @@ int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int
     a.T = K / 128;
     return hsq::hip_code(hsq::launch_rows(hsq::W_INT4, a, nblk, xl, ms, static_cast<hipStream_t>(stream)));
   }
-  if (M > 128 || !hsq::mid_ok(a, hsq::W_INT4)) return HS_EUNSUPPORTED;
+  if (M > 128) {
+    // Prefill: the 256x256-tile kernel's store carries the epilogue.
+    if (!hsq::wide_ok(a, hsq::W_INT4)) return HS_EUNSUPPORTED;
+    const hsq::Plan p = hsq::make_plan(hsq::W_INT4, M, N, K, false, false, true, false, false);
+    if (!p.wide || p.T > hsq::kMaxTiles) return HS_EUNSUPPORTED;
+    if (workspace == nullptr || workspace_bytes < p.ws_bytes) return HS_EWORKSPACE;
+    a.G = p.G;
+    a.NB = p.NB;
+    a.T = p.T;
+    a.TM = p.TM;
+    a.U = p.U;
+    a.P = p.P;
+    a.counters = reinterpret_cast<int*>(workspace);
+    a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.counter_bytes);
+    return hsq::hip_code(hsq::launch_wide(hsq::W_INT4, a, static_cast<hipStream_t>(stream)));
+  }
+  if (!hsq::mid_ok(a, hsq::W_INT4)) return HS_EUNSUPPORTED;
   const hsq::Plan p = hsq::make_plan(hsq::W_INT4, M, N, K, false, false, false, true, false);
   if (!p.mid) return HS_EUNSUPPORTED;
   if (p.T > hsq::kMaxTiles) return HS_EUNSUPPORTED;

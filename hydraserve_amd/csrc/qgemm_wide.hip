@@ -50,7 +50,7 @@ namespace hsq {
 
 constexpr int WD_THREADS = 256;
 
-template <int WT, int SDT>
+template <int WT, int SDT, bool SILU = false>
 struct Wide {
   static constexpr int BM = 256;
   static constexpr int BN = 256;
@@ -280,6 +280,25 @@ struct Wide {
     }
   }
 
+  // One output element (row m, column n < N) of lane l32 in the fused
+  // SiLU-and-mul instance (SILU, a.silu_mul): the weight rows interleave gate and up
+  // in 16-row blocks, so lane l32 < 16 of a 32-column block holds gate column
+  // g = 16*(n/32) + l32 and lane l32 + 16 the matching up column.  As in the
+  // reference's unfused sequence (hydraserve/model/runtime.py:1202-1210,
+  // silu_and_mul at hydraserve/kernels/activation.py:66-76), gate and up are
+  // rounded to bf16 first, then out = gate * sigmoid(gate) * up in fp32,
+  // rounded to bf16, into y [M, N/2].  Every lane of the wave calls this for
+  // the same (m, register) together, so the cross-lane exchange sees its
+  // partner; N is a multiple of 32, so a lane and its partner agree on n < N.
+  static __device__ __forceinline__ void put_silu(const GemmArgs& a, int m, int n, float v, int l32) {
+    const float own = bf16_to_f32(to_bf16_bits(v));
+    const float up = __shfl_xor(own, 16);
+    if (l32 < 16 && m < a.M) {
+      const float sig = 1.0f / (1.0f + __expf(-own));
+      a.y[m * a.ldy + (n >> 5) * 16 + (n & 15)] = to_bf16_bits(own * sig * up);
+    }
+  }
+
   // Lane (l32, h), register e of block (i, j): row 32i + 8(e/4) + 4h + e%4,
   // column 64*wave + 32j + l32.
   static __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&acc)[MI][2], int tm,
@@ -293,7 +312,11 @@ struct Wide {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int m = tm * BM + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-          if (m < a.M) a.y[m * a.ldy + n] = to_bf16_bits(acc[i][j][e]);
+          if constexpr (SILU) {
+            put_silu(a, m, n, acc[i][j][e], l32);
+          } else {
+            if (m < a.M) a.y[m * a.ldy + n] = to_bf16_bits(acc[i][j][e]);
+          }
         }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -365,7 +388,11 @@ struct Wide {
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int m = tm * BM + 32 * (i0 + ii) + 8 * (e >> 2) + 4 * h + (e & 3);
-            if (m < a.M && n < a.N) a.y[m * a.ldy + n] = to_bf16_bits(sum[ii][j][e]);
+            if constexpr (SILU) {
+              if (n < a.N) put_silu(a, m, n, sum[ii][j][e], l32);
+            } else {
+              if (m < a.M && n < a.N) a.y[m * a.ldy + n] = to_bf16_bits(sum[ii][j][e]);
+            }
           }
       }
     }
@@ -376,9 +403,9 @@ struct Wide {
 // a.G = 64-wide K units per tile, a.T = tiles, a.TM = tiles along M,
 // a.U = T * G, a.P = workgroups.  Tile t covers rows (t / (T/TM)) * 256 and
 // weight rows (t % (T/TM)) * 256.
-template <int WT, int SDT>
+template <int WT, int SDT, bool SILU>
 __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
-  using W = Wide<WT, SDT>;
+  using W = Wide<WT, SDT, SILU>;
   __shared__ typename W::Smem sm;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
@@ -478,9 +505,9 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
   }
 }
 
-template <int WT, int SDT>
+template <int WT, int SDT, bool SILU = false>
 static hipError_t launch_wide_t(const GemmArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((qgemm_wide_kernel<WT, SDT>), dim3(a.P), dim3(WD_THREADS), 0, stream, a);
+  hipLaunchKernelGGL((qgemm_wide_kernel<WT, SDT, SILU>), dim3(a.P), dim3(WD_THREADS), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -499,6 +526,12 @@ bool wide_ok(const GemmArgs& a, int wt) {
 }
 
 hipError_t launch_wide(int wt, const GemmArgs& a, hipStream_t stream) {
+  if (wt == W_INT4 && a.silu_mul) {
+    if (a.sdt == SCALE_BF16) return launch_wide_t<W_INT4, SCALE_BF16, true>(a, stream);
+    if (a.sdt == SCALE_F16) return launch_wide_t<W_INT4, SCALE_F16, true>(a, stream);
+    return launch_wide_t<W_INT4, SCALE_F32, true>(a, stream);
+  }
+  if (a.silu_mul) return hipErrorInvalidValue;
   if (wt == W_INT4) {
     if (a.sdt == SCALE_BF16) return launch_wide_t<W_INT4, SCALE_BF16>(a, stream);
     if (a.sdt == SCALE_F16) return launch_wide_t<W_INT4, SCALE_F16>(a, stream);

@@ -14,8 +14,8 @@ silu(gate) * up directly (hs_int4_gemm_silu_mul), skipping the [M, N] bf16
 round trip and the activation launch.  Gate and up are rounded to bf16 before
 the activation, as in the reference's unfused sequence.
 
-The fused store is in the row-partitioned decode kernels (1..16 rows) and in
-the 17..128-row streaming kernel.  Where
+The fused store is in the row-partitioned decode kernels (1..16 rows), the
+17..128-row streaming kernel and the 256x256-tile prefill kernel.  Where
 neither applies (e.g. more than 128 rows), awq_gate_up_silu_mul runs hs_int4_gemm on the interleaved weight and the
 activation as torch GPU ops on its output.
 """

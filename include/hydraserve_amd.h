@@ -80,8 +80,8 @@ int hs_int4_gemm(const void* x, int64_t ldx,
  * 16j..16j+15, then up rows 16j..16j+15: the load-time layout
  * hydraserve_amd.kernels.mlp.interleave_gate_up builds).  N (both halves) a
  * multiple of 32, ldy >= N/2; workspace as for hs_int4_gemm.  Returns
- * HS_EUNSUPPORTED above 128 rows, or when K or the strides do not suit the
- * kernels (K a multiple of 128; at 1..16 rows also at least 1024); the caller then runs hs_int4_gemm and the activation
+ * HS_EUNSUPPORTED when K or the strides do not suit the kernels (K a
+ * multiple of 128, 16-byte aligned rows; at 1..16 rows K at least 1024); the caller then runs hs_int4_gemm and the activation
  * separately. */
 int hs_int4_gemm_silu_mul(const void* x, int64_t ldx,
                           const int32_t* packed, int64_t ld_packed,

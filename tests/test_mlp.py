@@ -5,7 +5,8 @@ the oracle's unpack and dequantizer, and by its inverse), and the fused C
 entry point validates its arguments like hs_int4_gemm.
 GPU: hs_int4_gemm_silu_mul (1..16 rows in the block-major GEMV or the
 row-partitioned kernel,
-17..128 rows in the LDS-DMA streaming kernel) and the unfused fallback against
+17..128 rows in the LDS-DMA streaming kernel, from 129 rows in the 256x256-tile
+prefill kernel) and the unfused fallback against
 the oracle, with the bars of tests/test_gemm_gpu.py applied to
 silu(bf16(gate)) * bf16(up) computed from the float64 oracle GEMM, and
 against the product path's own unfused sequence (awq_linear on the original
@@ -84,7 +85,7 @@ def test_fused_entry_point_validates_arguments():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m", [1, 4, 7, 8, 12, 16, 17, 32, 64, 100, 128, 130])
+@pytest.mark.parametrize("m", [1, 4, 7, 8, 12, 16, 17, 32, 64, 100, 128, 130, 300])
 @pytest.mark.parametrize("n,k", [(2048, 1024), (1536, 640), (2048, 5120)])
 def test_fused_gate_up_silu_mul(m, n, k):
     if not torch.cuda.is_available():
@@ -100,7 +101,7 @@ def test_fused_gate_up_silu_mul(m, n, k):
     wi = interleave_gate_up(w)
     out = awq_gate_up_silu_mul(x, wi)
     torch.cuda.synchronize()
-    if m <= 128 and k % 128 == 0 and k // 128 >= 8:  # the fused entry point itself takes these
+    if k % 128 == 0 and k // 128 >= 8:  # the fused entry point itself takes these
         from hydraserve_amd import _native
 
         assert _native.int4_gemm_silu_mul(
