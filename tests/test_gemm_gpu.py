@@ -109,11 +109,11 @@ def int4_ref(x_bits, packed, scale_t, zero, n, k):
     z = qo.unpack_zero_points(zero, n).astype(np.int32)
     g = np.arange(k) // 128
     w_exact = (q - z[:, g]).astype(np.float64) * s[:, g]
-    w = (q - z[:, g]).astype(np.float32) * s[:, g]
-    if scale_t.dtype == torch.bfloat16:
-        w = qo.bf16_bits_to_f32(qo.f32_to_bf16_bits(w))
-    elif scale_t.dtype == torch.float16:
-        w = w.astype(np.float16).astype(np.float32)
+    # The GEMM kernel this path replaces rounds fp32((q - z) * s) to bf16 for
+    # every scale dtype (hydraserve/kernels/awq.py:136-137).
+    # (dequantize_int4_weight, awq.py:19-22, rounds to the scale dtype
+    # instead; that oracle is pinned bit-exact by its own tests.)
+    w = qo.bf16_bits_to_f32(qo.f32_to_bf16_bits((q - z[:, g]).astype(np.float32) * s[:, g]))
     x = qo.bf16_bits_to_f32(x_bits)
     ref = qo.gemm_f64(x, w).view(RefArray)
     ref.exact = x.astype(np.float64) @ w_exact.T
@@ -218,6 +218,21 @@ def test_int4_reference_case_seed41(golden_dir):
 
 
 MS = [1, 2, 3, 4, 8, 15, 16, 17, 31, 32, 33, 48, 63, 64, 65, 100, 128, 129, 200, 256, 300]
+
+
+# fp16 and fp32 scales through every regime at a serving-sized K: the
+# row-partitioned and register-streamed decode kernels (exact group rewrite),
+# the 17..128-row streaming kernel and the 256x256 prefill kernel (weights
+# rounded to bf16 as at hydraserve/kernels/awq.py:136-137)
+@pytest.mark.parametrize("m", [4, 16, 64, 300])
+@pytest.mark.parametrize("sdt", [torch.float16, torch.float32])
+def test_int4_gemm_scale_dtypes(m, sdt):
+    dev = _cuda()
+    rng = np.random.default_rng(500 + m)
+    n, k = 2048, 5120
+    w, x, x_bits, packed, scale, zero, _ = int4_case(rng, m, n, k, dev, sdt)
+    y = hs.awq_linear(x, w)
+    assert_gemm_close(y, int4_ref(x_bits, packed, scale, zero, n, k), what=f"m={m} scales={sdt}")
 
 
 @pytest.mark.parametrize("m", MS)

@@ -88,6 +88,20 @@ def test_fused_entry_point_validates_arguments():
 @pytest.mark.parametrize("m", [1, 4, 7, 8, 12, 16, 17, 32, 64, 100, 128, 130, 300])
 @pytest.mark.parametrize("n,k", [(2048, 1024), (1536, 640), (2048, 5120)])
 def test_fused_gate_up_silu_mul(m, n, k):
+    _check_fused(m, n, k, torch.bfloat16)
+
+
+# fp16 and fp32 scales run their own instances of every fused kernel (block-
+# major and row-partitioned decode at 4 and 16 rows, streaming at 64, prefill
+# at 300)
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [4, 16, 64, 300])
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+def test_fused_gate_up_silu_mul_scale_dtypes(m, scale_dtype):
+    _check_fused(m, 2048, 5120, scale_dtype)
+
+
+def _check_fused(m, n, k, scale_dtype):
     if not torch.cuda.is_available():
         pytest.skip("needs a ROCm GPU")
     import hydraserve_amd as hs
@@ -97,7 +111,7 @@ def test_fused_gate_up_silu_mul(m, n, k):
 
     dev = torch.device("cuda", 0)
     rng = np.random.default_rng(7000 + m)
-    w, x, xb, packed, scale, zero, _ = tg.int4_case(rng, m, n, k, dev)
+    w, x, xb, packed, scale, zero, _ = tg.int4_case(rng, m, n, k, dev, scale_dtype)
     wi = interleave_gate_up(w)
     out = awq_gate_up_silu_mul(x, wi)
     torch.cuda.synchronize()
@@ -120,7 +134,7 @@ def test_fused_gate_up_silu_mul(m, n, k):
 
     ref = act(y).view(tg.RefArray)
     ref.exact = act(y.exact)
-    tg.assert_gemm_close(out, ref, what=f"fused silu_mul M={m} N={n} K={k}")
+    tg.assert_gemm_close(out, ref, what=f"fused silu_mul M={m} N={n} K={k} scales={scale_dtype}")
     # the product path's unfused sequence on the original weight
     gate, up = hs.awq_linear(x, w).chunk(2, dim=-1)
     unfused = silu_and_mul(gate.contiguous(), up.contiguous())
