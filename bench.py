@@ -202,7 +202,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep-json", metavar="PATH", help="with --sweep: also write the result to PATH")
     ap.add_argument("--profile", metavar="KIND:SHAPE:M",
-                    help="eager launches of one GEMM (e.g. int4:gate_up:64) plus a plain copy kernel of "
+                    help="eager launches of one GEMM (e.g. int4:gate_up:64; int4silu:gate_up:M for the fused "
+                    "SiLU-and-mul store) plus a plain copy kernel of "
                     "known size, for rocprofv3 counter passes; prints one JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -317,13 +318,25 @@ def profile(torch, gen, dev, spec, launches):
     kind, name, m = spec.split(":")
     n, k = SHAPES[name]
     m = int(m)
+    # kind "int4silu": gate_up with the fused SiLU-and-mul store, on weights
+    # interleaved at load time (awq_gate_up_silu_mul)
+    fused = kind == "int4silu"
+    if fused:
+        kind = "int4"
     make = make_int4 if kind == "int4" else make_fp8
     per_copy = int4_bytes(n, k) if kind == "int4" else fp8_bytes(n, k)
     ws = make(torch, n, k, copies_for(per_copy), gen, dev)
     x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
+    if fused:
+        from hydraserve_amd.kernels import awq_gate_up_silu_mul, interleave_gate_up
+
+        ws = [interleave_gate_up(w) for w in ws]
     c = Case(kind, name, n, k, m, ws, x)
     for i in range(launches):
-        c.call(i)
+        if fused:
+            awq_gate_up_silu_mul(x, ws[i % len(ws)])
+        else:
+            c.call(i)
     src = torch.empty(COPY_CAL_BYTES, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(4):
