@@ -1,26 +1,31 @@
 """Benchmark of the quantized linear-layer hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--sweep] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--headline-only] [--sweep]
 
 Headline workload: INT4 group-128 asymmetric decode GEMMs,
 M in {1, 4, 16, 64} x {gate_up 5120->34816, down 17408->5120}.  One "step" is
 one pass over those 8 GEMMs through the product entry point
 (hydraserve_amd.awq_linear -> C ABI -> HIP).  Inputs are synthetic and
 resident in HBM before timing; weights rotate over several independent copies
-(> 256 MB MALL) so every GEMM streams its weights from HBM.  Steps are
-captured in a HIP graph (as the reference's decode loop does,
-hydraserve/model/runtime.py:788-803) and timed with events around graph
-replays, bracketed by synchronizations.
+(> 256 MB MALL) so every GEMM streams its weights from HBM.  W eager warmup
+steps run first; then exactly K steps are captured in one HIP graph (as the
+reference's decode loop captures its step, hydraserve/model/runtime.py:788-803),
+replayed once untimed and once between two events, bracketed by
+synchronizations.
 
 `value` = weight bytes (packed + scale + zero) of all GEMMs / step time, GB/s.
-`roofline` = the dominant kernel's algorithmic weight bytes / its mean launch
-duration (events around graph replays of back-to-back launches of that GEMM).
+`roofline` = the dominant config-1 kernel's algorithmic weight bytes / its mean
+launch duration (events around graph replays of back-to-back launches of that
+GEMM), next to the streaming-read ceiling measured by hs_hbm_read_probe.
+`per_shape` = every BASELINE config (0: INT4 4096^2 M=8; 1; 2: INT4 prefill;
+3: FP8 decode + prefill; 4: the decoder layer's five projections at M=64/1024,
+summed in `config4_layer`), each with its regime's roofline fraction (HBM for
+M <= 64, bf16 MFMA above); `roofline_prefill` = the dominant prefill kernel.
 `cpu_baseline` = the reference's CPU torch path (dequant + bf16 matmul,
-oracle/torch_cpu_path.py) timed on a bounded sample on the host cores.
+oracle/torch_cpu_path.py), INT4 and FP8, timed on the host cores.
 
---sweep additionally measures every BASELINE config (INT4/FP8, decode and
-prefill, the config-4 layer) and prints one JSON object per shape to stderr;
---sweep-json PATH also writes the whole result there.
+--sweep adds the fused gate_up + SiLU-and-mul comparison; --sweep-json PATH
+writes the whole result there as well.
 """
 
 from __future__ import annotations
@@ -155,42 +160,143 @@ class Case:
         }
 
 
-def cpu_baseline(sample_shapes, m):
-    """Reference CPU path on the host: dequant + bf16 matmul per call (kind 'port')."""
+def cpu_baseline(m, reps=3):
+    """Reference CPU path on the host: dequant + bf16 matmul per call (kind 'port'),
+    INT4 and FP8 on the config-1/3 shapes at M=m; per shape the median of `reps`
+    timed calls after one warmup."""
+    import statistics
+
     import torch
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle.torch_cpu_path import int4_cpu_linear
+    from oracle.torch_cpu_path import fp8_cpu_linear, int4_cpu_linear
 
     cores = os.cpu_count() or 1
     cores = min(cores, int(os.environ.get("HS_CPU_THREADS", cores)))
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(0)
-    total_bytes, total_s = 0, 0.0
-    for (n, k) in sample_shapes:
-        gg = (k + 127) // 128
-        packed = torch.randint(-(2**31), 2**31 - 1, (n, k // 8), generator=g, dtype=torch.int32)
-        zero = torch.randint(-(2**31), 2**31 - 1, ((n + 7) // 8, gg), generator=g, dtype=torch.int32)
-        scale = (torch.rand(n, gg, generator=g) * 9e-3 + 1e-3).to(torch.bfloat16)
-        x = torch.randn(m, k, generator=g).to(torch.bfloat16)
-        int4_cpu_linear(x, packed, scale, zero, (n, k))  # warmup
-        times = []
-        for _ in range(2):
-            t0 = time.perf_counter()
-            int4_cpu_linear(x, packed, scale, zero, (n, k))
-            times.append(time.perf_counter() - t0)
-        total_s += min(times)
-        total_bytes += int4_bytes(n, k)
-        del packed, zero, scale
+    per, total_bytes, total_s = [], 0, 0.0
+    for kind in ("int4", "fp8"):
+        for name, (n, k) in (("gate_up", GATE_UP), ("down", DOWN)):
+            x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+            if kind == "int4":
+                gg = (k + 127) // 128
+                packed = torch.randint(-(2**31), 2**31 - 1, (n, k // 8), generator=g, dtype=torch.int32)
+                zero = torch.randint(-(2**31), 2**31 - 1, ((n + 7) // 8, gg), generator=g, dtype=torch.int32)
+                scale = (torch.rand(n, gg, generator=g) * 9e-3 + 1e-3).to(torch.bfloat16)
+
+                def call():
+                    return int4_cpu_linear(x, packed, scale, zero, (n, k))
+
+                nbytes = int4_bytes(n, k)
+            else:
+                data = torch.randint(0, 254, (n, k), generator=g, dtype=torch.int32)
+                data = torch.where(data >= 0x7F, data + 1, data).to(torch.uint8).view(torch.float8_e4m3fn)
+                sinv = torch.rand((n + 127) // 128, (k + 127) // 128, generator=g) * 0.099 + 0.001
+
+                def call():
+                    return fp8_cpu_linear(x, data, sinv, (n, k))
+
+                nbytes = fp8_bytes(n, k)
+            call()  # warmup
+            times = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                call()
+                times.append(time.perf_counter() - t0)
+            med = statistics.median(times)
+            per.append({"kind": kind, "shape": name, "M": m, "ms": round(med * 1e3, 1),
+                        "weight_GBps": round(nbytes / med / 1e9, 3)})
+            total_s += med
+            total_bytes += nbytes
+            del call
     return {
         "value": round(total_bytes / total_s / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"INT4 dequant+bf16 matmul (reference CPU branch) at M={m} on "
-        + ", ".join(f"{n}x{k}" for n, k in sample_shapes)
-        + f"; best of 2 after 1 warmup; {total_s * 1e3:.0f} ms per pass",
+        "sample": f"reference CPU branch (dequant + bf16 matmul per call, awq.py:36-38 / fp8.py:51-53) at M={m} "
+        "on INT4 and FP8 gate_up 5120->34816 and down 17408->5120; median of "
+        f"{reps} calls after 1 warmup per shape; {total_s * 1e3:.0f} ms for the four medians",
+        "per_shape": per,
     }
+
+
+def hbm_ceiling(torch, dev, nbytes=4 << 30):
+    """Streaming-read ceiling: hs_hbm_read_probe over a 4 GiB buffer (far past
+    the 256 MB MALL), best over a few grid sizes; events on the launch stream."""
+    from hydraserve_amd import _native
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    src.fill_(1)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    best = None
+    for per_cu in (2, 4, 8, 16):
+        blocks = cus * per_cu
+        sink = torch.empty(blocks, dtype=torch.int32, device=dev)
+        _native.hbm_read_probe(src, sink, blocks)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 5
+        start.record()
+        for _ in range(reps):
+            _native.hbm_read_probe(src, sink, blocks)
+        end.record()
+        torch.cuda.synchronize()
+        gbs = nbytes * reps / (start.elapsed_time(end) * 1e-3) / 1e9
+        if best is None or gbs > best[0]:
+            best = (gbs, blocks)
+    del src
+    torch.cuda.empty_cache()
+    return {"GBps": round(best[0], 1), "bytes": nbytes, "workgroups": best[1]}
+
+
+# Every BASELINE config as (config, kind, shape, M list); configs 1 and 4 share
+# gate_up/down at M=64.
+ALL_CONFIGS = [
+    ("c0", "int4", "c0", [8]),
+    ("c1", "int4", "gate_up", [1, 4, 16, 64]),
+    ("c1", "int4", "down", [1, 4, 16, 64]),
+    ("c2", "int4", "gate_up", [512, 2048]),
+    ("c2", "int4", "down", [512, 2048]),
+    ("c3", "fp8", "gate_up", [1, 16, 256, 2048]),
+    ("c3", "fp8", "down", [1, 16, 256, 2048]),
+    ("c4", "int4", "gate_up", [1024]),
+    ("c4", "int4", "down", [1024]),
+    ("c4", "int4", "qkv", [64, 1024]),
+    ("c4", "int4", "o_proj", [64, 1024]),
+    ("c4", "int4", "gdn_in", [64, 1024]),
+]
+
+
+def measure_all(torch, gen, dev):
+    """One timed entry per (config, shape, M): graphs of back-to-back launches
+    over rotated weight copies, HIP events around the replays."""
+    out = []
+    for cfg, kind, name, m_list in ALL_CONFIGS:
+        n, k = SHAPES[name]
+        make = make_int4 if kind == "int4" else make_fp8
+        per_copy = int4_bytes(n, k) if kind == "int4" else fp8_bytes(n, k)
+        copies = copies_for(per_copy)
+        ws = make(torch, n, k, copies, gen, dev)
+        for m in m_list:
+            x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
+            c = Case(kind, name, n, k, m, ws, x)
+            reps = 10 if m <= 64 else 4
+            ms, _ = graph_time_ms(torch, c.call, reps, 2 * copies)
+            r = c.report(ms)
+            r["config"] = cfg
+            out.append(r)
+            print(json.dumps(r), file=sys.stderr, flush=True)
+        del ws
+        torch.cuda.empty_cache()
+    # config 4: summed latency of one decoder layer's projections
+    layer = {}
+    for r in out:
+        if r["kind"] == "int4" and r["shape"] in ("qkv", "o_proj", "gdn_in", "gate_up", "down") and r["M"] in (64, 1024):
+            layer.setdefault(r["M"], []).append(r["us"])
+    c4 = {str(m): {"us": round(sum(v), 2), "linears": len(v)} for m, v in sorted(layer.items())}
+    return out, c4
 
 
 def main():
@@ -198,9 +304,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--warmup", type=int, default=6)
-    ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--sweep", action="store_true", help="also the fused gate_up+SiLU comparison")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--sweep-json", metavar="PATH", help="with --sweep: also write the result to PATH")
+    ap.add_argument("--headline-only", action="store_true", help="skip the per-config entries")
+    ap.add_argument("--sweep-json", metavar="PATH", help="also write the whole result there")
     ap.add_argument("--profile", metavar="KIND:SHAPE:M",
                     help="eager launches of one GEMM (e.g. int4:gate_up:64; int4silu:gate_up:M for the fused "
                     "SiLU-and-mul store) plus a plain copy kernel of "
@@ -241,13 +348,31 @@ def main():
         for c in cases:
             c.call(i)
 
-    # warmup (eager) then one graph holding `copies` steps (each on another copy)
+    # W eager warmup steps, then one graph of exactly K steps (step i on
+    # weight copy i mod copies), replayed once untimed and once timed.
+    steps = max(1, args.steps)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    reps = max(1, -(-args.steps // copies))
-    steps = reps * copies
-    t_ms, _ = graph_time_ms(torch, step, reps, copies)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            step(i)
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    t_ms = start.elapsed_time(end) / steps
+    del g
     step_bytes = sum(c.wbytes for c in cases)
     step_flops = sum(c.flops for c in cases)
     value = step_bytes / (t_ms * 1e-3) / 1e9
@@ -256,8 +381,13 @@ def main():
     per = []
     for c in cases:
         ms, _ = graph_time_ms(torch, c.call, 10, 2 * copies)
-        per.append((c, ms, c.report(ms)))
+        r = c.report(ms)
+        r["config"] = "c1"
+        per.append((c, ms, r))
+    del weights, cases, xs
+    torch.cuda.empty_cache()
     dom_c, dom_ms, dom_r = max(per, key=lambda t: t[1])
+    ceiling = hbm_ceiling(torch, dev)
     roofline = {
         "bound": "hbm",
         "achieved": dom_r["weight_GBps"],
@@ -268,6 +398,9 @@ def main():
         "kernel": f"INT4 decode {dom_c.name} M={dom_c.m} ({dom_c.n}x{dom_c.k})",
         "bytes_per_launch": dom_c.wbytes,
         "us_per_launch": dom_r["us"],
+        "measured_ceiling_GBps": ceiling["GBps"],
+        "frac_of_measured_ceiling": round(dom_r["weight_GBps"] / ceiling["GBps"], 4),
+        "ceiling_probe": ceiling,
     }
 
     result = {
@@ -282,27 +415,45 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (uniform int4 nibbles/zero points, bf16 scales U[1e-3,1e-2], X~N(0,1)); "
-        f"weights rotated over {copies} copies",
+        "data": "synthetic (uniform int4 nibbles/zero points, bf16 scales U[1e-3,1e-2], X~N(0,1); FP8 uniform "
+        f"finite E4M3FN codes, fp32 block scales U[1e-3,1e-1]); weights rotated over >= {copies} copies",
         "config": {
             "workload": "config 1: INT4 g128 asymmetric decode GEMMs, M in {1,4,16,64} x "
             "{gate_up 5120->34816, down 17408->5120}, 8 GEMMs per step",
             "weight_bytes_per_step": step_bytes,
             "tflops": round(step_flops / (t_ms * 1e-3) / 1e12, 3),
             "weight_copies": copies,
-            "launch": "HIP graph replay",
+            "launch": "HIP graph of K steps, replayed once",
         },
         "roofline": roofline,
         "per_shape": [r for _, _, r in per],
     }
 
+    if not args.headline_only:
+        entries, c4 = measure_all(torch, gen, dev)
+        result["per_shape"] += entries
+        result["config4_layer"] = c4
+        prefill = [r for r in entries if r["bound"] == "mfma"]
+        dom_p = max(prefill, key=lambda r: r["us"])
+        result["roofline_prefill"] = {
+            "bound": "mfma",
+            "achieved": dom_p["TFLOPs"],
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": dom_p["roofline_frac"],
+            "traffic": None,
+            "kernel": f"{dom_p['kind'].upper()} prefill {dom_p['shape']} M={dom_p['M']} ({dom_p['N']}x{dom_p['K']})",
+            "flops_per_launch": 2 * dom_p["M"] * dom_p["N"] * dom_p["K"],
+            "us_per_launch": dom_p["us"],
+        }
+
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline([GATE_UP, DOWN], 16)
+        result["cpu_baseline"] = cpu_baseline(16)
 
     if args.sweep:
         result["sweep"] = sweep(torch, gen, dev)
     print(json.dumps(result), flush=True)
-    if args.sweep and args.sweep_json:
+    if args.sweep_json:
         with open(args.sweep_json, "w") as f:
             json.dump(result, f, indent=1)
 
@@ -347,29 +498,8 @@ def profile(torch, gen, dev, spec, launches):
 
 
 def sweep(torch, gen, dev):
+    """gate_up followed by SiLU-and-mul: fused epilogue vs the reference's sequence."""
     out = []
-
-    def run(kind, name, n, k, m_list):
-        make = make_int4 if kind == "int4" else make_fp8
-        per_copy = int4_bytes(n, k) if kind == "int4" else fp8_bytes(n, k)
-        copies = copies_for(per_copy)
-        ws = make(torch, n, k, copies, gen, dev)
-        for m in m_list:
-            x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
-            c = Case(kind, name, n, k, m, ws, x)
-            reps = 10 if m <= 64 else 4
-            ms, _ = graph_time_ms(torch, c.call, reps, copies)
-            r = c.report(ms)
-            print(json.dumps(r), file=sys.stderr, flush=True)
-            out.append(r)
-        del ws
-        torch.cuda.empty_cache()
-
-    run("int4", "c0", *C0, [8])
-    run("int4", "gate_up", *GATE_UP, [1, 4, 16, 64, 512, 1024, 2048])
-    run("int4", "down", *DOWN, [1, 4, 16, 64, 512, 1024, 2048])
-    run("fp8", "gate_up", *GATE_UP, [1, 16, 256, 2048])
-    run("fp8", "down", *DOWN, [1, 16, 256, 2048])
     # gate_up followed by SiLU-and-mul: fused epilogue on the interleaved
     # weight vs the reference's sequence (GEMM, chunk, activation launch).
     from hydraserve_amd.kernels import awq_gate_up_silu_mul, interleave_gate_up, silu_and_mul
@@ -397,16 +527,6 @@ def sweep(torch, gen, dev):
         out.append(r)
     del ws, wis
     torch.cuda.empty_cache()
-    run("int4", "qkv", *QKV, [64, 1024])
-    run("int4", "o_proj", *O_PROJ, [64, 1024])
-    run("int4", "gdn_in", *GDN_IN, [64, 1024])
-    layer = {}
-    for r in out:
-        if r["kind"] == "int4" and r["shape"] in ("qkv", "o_proj", "gdn_in", "gate_up", "down") and r["M"] in (64, 1024):
-            layer.setdefault(r["M"], 0.0)
-            layer[r["M"]] += r["us"]
-    out.append({"config4_layer_us": {str(m): round(v, 2) for m, v in layer.items()}})
-    print(json.dumps(out[-1]), file=sys.stderr, flush=True)
     return out
 
 

@@ -9,6 +9,7 @@ Public surface mirrors the reference's:
 All compute runs in libhydraserve_amd.so (hand-written HIP for gfx950).
 """
 
+from . import ops  # noqa: F401  (registers the torch.library custom ops)
 from .kernels import awq_linear, dequantize_fp8_weight, dequantize_int4_weight, fp8_linear
 from .model.linear import concatenate_linear_weights, linear, split_linear_weight
 from .model.weights import BlockScaledFP8Weight, PackedInt4Weight

@@ -34,6 +34,7 @@ SIGNATURES = {
     "hs_fp8_gemm": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _I, _I, _I, _P, _I64, _P]),
     "hs_int4_dequant": (_I, [_P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
     "hs_fp8_dequant": (_I, [_P, _I64, _P, _I64, _I, _P, _I64, _I, _I, _I, _P]),
+    "hs_hbm_read_probe": (_I, [_P, _I64, _P, _I64, _I, _P]),
 }
 ABI_VERSION = 1
 
@@ -220,3 +221,15 @@ def fp8_dequant(data_u8, scale_inv, n: int, k: int, out_dtype):
         "hs_fp8_dequant",
     )
     return out
+
+
+def hbm_read_probe(src, sink, blocks: int) -> None:
+    """One streaming read of every byte of ``src`` (a contiguous CUDA tensor)."""
+    import torch
+
+    stream = torch.cuda.current_stream(src.device).cuda_stream
+    nbytes = src.numel() * src.element_size()
+    check(
+        lib().hs_hbm_read_probe(src.data_ptr(), nbytes, sink.data_ptr(), sink.numel() * sink.element_size(), blocks, stream),
+        "hs_hbm_read_probe",
+    )

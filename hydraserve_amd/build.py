@@ -19,7 +19,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libhydraserve_amd.so"
 BUILD_DIR = PKG / "_build"
-SOURCES = ["qgemm_skinny.hip", "qgemm_decode.hip", "qgemm_stream.hip", "qgemm_rows.hip", "qgemm_gemv.hip", "qgemm_prefill.hip", "qgemm_wide.hip", "qgemm_mid.hip", "qgemm_dequant.hip", "qgemm_capi.hip"]
+SOURCES = ["qgemm_skinny.hip", "qgemm_decode.hip", "qgemm_stream.hip", "qgemm_rows.hip", "qgemm_gemv.hip", "qgemm_prefill.hip", "qgemm_wide.hip", "qgemm_mid.hip", "qgemm_dequant.hip", "hbm_probe.hip", "qgemm_capi.hip"]
 ARCH = os.environ.get("HS_OFFLOAD_ARCH", "gfx950")
 
 

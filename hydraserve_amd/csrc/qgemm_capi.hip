@@ -304,7 +304,30 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 bool valid_dt(int dt) { return dt == HS_DT_BF16 || dt == HS_DT_F16 || dt == HS_DT_F32; }
 
+// Every kernel addresses its operands through buffer resources whose range
+// and per-lane offsets are 32-bit.  An operand spanning 2^31 bytes or more
+// would get a wrapped range, and out-of-range buffer loads read zero without
+// a fault, so such calls are refused here instead of computing wrong values.
+bool extents_ok(int wt, const GemmArgs& a, int y_cols) {
+  constexpr int64_t lim = int64_t(1) << 31;
+  const int64_t groups = (a.K + 127) / 128;
+  const int64_t ses = a.sdt == HS_DT_F32 ? 4 : 2;
+  const int64_t xb = ((a.M - 1) * a.ldx + a.K) * 2;
+  const int64_t yb = ((a.M - 1) * a.ldy + y_cols) * 2;
+  int64_t wb, sb, zb = 0;
+  if (wt == W_INT4) {
+    wb = ((a.N - 1) * a.ldw + (a.K + 7) / 8) * 4;
+    sb = ((a.N - 1) * a.lds + groups) * ses;
+    zb = (((a.N + 7) / 8 - 1) * a.ldz + groups) * 4;
+  } else {
+    wb = (a.N - 1) * a.ldw + a.K;
+    sb = (((a.N + 127) / 128 - 1) * a.lds + groups) * ses;
+  }
+  return xb < lim && yb < lim && wb < lim && sb < lim && zb < lim;
+}
+
 int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  if (!extents_ok(wt, a, a.N)) return HS_EUNSUPPORTED;
   a.xvec = aligned16(a.x) && (a.ldx % 8 == 0);
   const Tuning& tn = tuning();
   // Decode with at most 16 activation rows: row-partitioned kernels, one
@@ -465,6 +488,7 @@ int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int
   a.wvec = hsq::aligned16(packed) && (ld_packed % 4 == 0);
   a.tune = hsq::tuning().tune;
   a.silu_mul = 1;
+  if (!hsq::extents_ok(hsq::W_INT4, a, N / 2)) return HS_EUNSUPPORTED;
   // The fused epilogue is in the block-major GEMV kernel (1..16 rows, X in
   // LDS) and in the 17..128-row LDS-DMA kernel.
   if (M <= 16) {

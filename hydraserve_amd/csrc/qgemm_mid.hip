@@ -245,7 +245,7 @@ struct Mid {
       const float up = __shfl_xor(own, 16);
       const int m = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
       if (l32 < 16 && m < a.M && n < a.N) {
-        const float sig = 1.0f / (1.0f + __expf(-own));
+        const float sig = 1.0f / (1.0f + expf(-own));
         a.y[m * a.ldy + col] = to_bf16_bits(own * sig * up);
       }
     }

@@ -96,7 +96,8 @@ template <int B>
 using Blob = typename VecT<B>::type;
 
 // Raw buffer access: a resource descriptor in SGPRs covering `bytes` bytes
-// from p (the host keeps every operand under 2^31 bytes), a per-lane 32-bit
+// from p (the host refuses calls with an operand of 2^31 bytes or more:
+// extents_ok in qgemm_capi.hip), a per-lane 32-bit
 // offset and a uniform 32-bit offset.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), static_cast<int>(bytes),

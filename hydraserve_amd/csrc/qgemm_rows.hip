@@ -366,7 +366,7 @@ __global__ __launch_bounds__(64 * KW) void qgemm_rows_kernel(GemmArgs a) {
         if (m < a.M) {
           const float gb = bf16_to_f32(to_bf16_bits(g[e]));
           const float ub = bf16_to_f32(to_bf16_bits(u[e]));
-          const float sig = 1.0f / (1.0f + __expf(-gb));
+          const float sig = 1.0f / (1.0f + expf(-gb));
           a.y[m * a.ldy + col] = to_bf16_bits(gb * sig * ub);
         }
       }

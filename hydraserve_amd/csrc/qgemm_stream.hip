@@ -650,6 +650,14 @@ int stream_slot_floats(int MT, int S) { return 4 * S * MT * 4 * 64; }
 // stride must be aligned to that vector.
 bool stream_ok(const GemmArgs& a, int wt, int NB) {
   if (a.M < 1 || a.M > 64 || !a.xvec || !a.wvec || a.K % (128 * NB) != 0) return false;
+  // Byte extents of every operand (with the tile overhang the kernel's
+  // clamped row indices can reach) stay below the 32-bit buffer range.
+  const int64_t lim = int64_t(1) << 31;
+  const int64_t xb = (static_cast<int64_t>(a.M) * a.ldx + a.K) * 2;
+  const int64_t wb = (static_cast<int64_t>(a.N) + 256) * a.ldw * (wt == W_INT4 ? 4 : 1);
+  const int64_t sb = (static_cast<int64_t>(a.N) + 256) * a.lds * 4;
+  const int64_t zb = (static_cast<int64_t>(a.N / 8) + 64) * a.ldz * 4;
+  if (xb >= lim || wb >= lim || sb >= lim || zb >= lim) return false;
   const int ses = a.sdt == SCALE_F32 ? 4 : 2;
   const int sbytes = NB * ses;  // scale bytes per batch per row
   const int salign = sbytes >= 16 ? 16 : sbytes;

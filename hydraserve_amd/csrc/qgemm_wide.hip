@@ -294,7 +294,7 @@ struct Wide {
     const float own = bf16_to_f32(to_bf16_bits(v));
     const float up = __shfl_xor(own, 16);
     if (l32 < 16 && m < a.M) {
-      const float sig = 1.0f / (1.0f + __expf(-own));
+      const float sig = 1.0f / (1.0f + expf(-own));
       a.y[m * a.ldy + (n >> 5) * 16 + (n & 15)] = to_bf16_bits(own * sig * up);
     }
   }

@@ -76,8 +76,14 @@ def awq_linear(hidden, weight):
     if flattened.dtype != torch.bfloat16:
         raise TypeError("hydraserve_amd quantized GEMMs take bfloat16 activations")
     n, k = weight.original_shape
+    if k == 0:
+        return torch.zeros(shape, device=hidden.device, dtype=hidden.dtype)
+    if torch.compiler.is_compiling():
+        # Dynamo/Inductor: the opaque custom op (hydraserve_amd/ops.py)
+        out = torch.ops.hydraserve_amd.int4_gemm(
+            flattened, weight.packed, weight.scale, weight.zero_point, n, k, weight.group_size
+        )
+        return out.reshape(shape)
     with device_guard(hidden.device):
-        if k == 0:
-            return torch.zeros(shape, device=hidden.device, dtype=hidden.dtype)
         out = _native.int4_gemm(flattened, weight.packed, weight.scale, weight.zero_point, n, k, weight.group_size)
     return out.reshape(shape)

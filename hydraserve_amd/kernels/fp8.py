@@ -84,8 +84,12 @@ def fp8_linear(hidden, weight):
     if flattened.dtype != torch.bfloat16:
         raise TypeError("hydraserve_amd quantized GEMMs take bfloat16 activations")
     _native.dtype_code(weight.scale_inv.dtype)
+    if input_features == 0:
+        return torch.zeros(shape, device=hidden.device, dtype=hidden.dtype)
+    if torch.compiler.is_compiling():
+        # Dynamo/Inductor: the opaque custom op (hydraserve_amd/ops.py)
+        out = torch.ops.hydraserve_amd.fp8_gemm(flattened, data, weight.scale_inv, output_features, input_features)
+        return out.reshape(shape)
     with device_guard(hidden.device):
-        if input_features == 0:
-            return torch.zeros(shape, device=hidden.device, dtype=hidden.dtype)
         out = _native.fp8_gemm(flattened, data, weight.scale_inv, output_features, input_features)
     return out.reshape(shape)

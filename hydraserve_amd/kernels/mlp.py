@@ -113,15 +113,23 @@ def awq_gate_up_silu_mul(hidden, weight: PackedInt4Weight):
     if flattened.dtype != torch.bfloat16:
         raise TypeError("hydraserve_amd quantized GEMMs take bfloat16 activations")
     shape = hidden.shape[:-1] + (n // 2,)
-    m = flattened.shape[0]
+    if k == 0:
+        return torch.zeros(shape, device=hidden.device, dtype=hidden.dtype)
+    args = (flattened, weight.packed, weight.scale, weight.zero_point, n, k, weight.group_size)
+    if torch.compiler.is_compiling():
+        # Dynamo/Inductor: the opaque custom op (hydraserve_amd/ops.py)
+        return torch.ops.hydraserve_amd.int4_gate_up_silu_mul(*args).reshape(shape)
     with device_guard(hidden.device):
-        if k == 0:
-            return torch.zeros(shape, device=hidden.device, dtype=hidden.dtype)
-        out = _native.int4_gemm_silu_mul(
-            flattened, weight.packed, weight.scale, weight.zero_point, n, k, weight.group_size
-        )
+        out = _native.int4_gemm_silu_mul(*args)
         if out is None:
-            y = _native.int4_gemm(flattened, weight.packed, weight.scale, weight.zero_point, n, k, weight.group_size)
-            pairs = y.view(m, n // (2 * BLOCK), 2, BLOCK)
-            out = silu_and_mul(pairs[:, :, 0], pairs[:, :, 1]).reshape(m, n // 2)
+            out = unfused_gate_up_silu_mul(*args)
     return out.reshape(shape)
+
+
+def unfused_gate_up_silu_mul(x, packed, scale, zero_point, n, k, group):
+    """The GEMM on the interleaved weight, then the activation on its gate/up
+    block pairs: for shapes the fused store does not cover."""
+    m = x.shape[0]
+    y = _native.int4_gemm(x, packed, scale, zero_point, n, k, group)
+    pairs = y.view(m, n // (2 * BLOCK), 2, BLOCK)
+    return silu_and_mul(pairs[:, :, 0], pairs[:, :, 1]).reshape(m, n // 2)

@@ -7,12 +7,19 @@ quantized path:
 * ``concatenate_linear_weights`` -> _concatenate_linear_weights (runtime.py:1404-1475)
 * ``split_linear_weight``        -> _split_linear_weight (runtime.py:1477-1506)
 
-Fusion concatenates packed INT4 / E4M3 storage along N without requantizing;
-splits are ``narrow`` views of the fused tensors, which the kernels read
-through their row strides.
+Fusion works on a per-format storage table: every quantized format is a set
+of tensors whose dim 0 indexes output rows at some granularity (one packed
+INT4 row per weight row, one zero-point word per 8 rows, one FP8 scale row
+per 128-row block, ...).  Concatenating along N is then a field-wise
+``torch.cat``, legal when every part's row count is a multiple of the
+format's coarsest granularity; splitting is a field-wise ``narrow`` (a view,
+which the kernels read through their row strides).  Nothing is requantized.
 """
 
 from __future__ import annotations
+
+import dataclasses
+import math
 
 from ..kernels.awq import awq_linear
 from ..kernels.fp8 import fp8_linear
@@ -20,6 +27,8 @@ from .weights import BlockScaledFP8Weight, PackedInt4Weight
 
 
 def linear(hidden, weight):
+    """isinstance dispatch of runtime.py:1263-1270: INT4 -> awq_linear, FP8 ->
+    fp8_linear, dense -> ``hidden @ weight.T`` on the weight's device."""
     if isinstance(weight, PackedInt4Weight):
         return awq_linear(hidden, weight)
     if isinstance(weight, BlockScaledFP8Weight):
@@ -29,104 +38,79 @@ def linear(hidden, weight):
     return hidden @ weight.transpose(0, 1)
 
 
+def _storage(weight) -> dict[str, int]:
+    """Tensor fields of a quantized weight -> weight rows covered by one row of
+    that tensor.  The key set also fixes which fields fusion concatenates."""
+    if isinstance(weight, PackedInt4Weight):
+        return {"packed": 1, "scale": 1, "zero_point": 8}
+    if isinstance(weight, BlockScaledFP8Weight):
+        return {"data": 1, "scale_inv": weight.block_size[0]}
+    raise TypeError(f"unsupported fused linear weight: {type(weight)!r}")
+
+
+def _static(weight) -> tuple:
+    """Everything besides the row count that fused parts must share."""
+    if isinstance(weight, PackedInt4Weight):
+        return (weight.original_shape[1], weight.group_size)
+    return (weight.original_shape[1], weight.block_size)
+
+
+def _tensor_key(t) -> tuple:
+    return (t.device, t.dtype)
+
+
 def concatenate_linear_weights(parts):
-    """Fuse projections along N; ``None`` when the parts cannot be fused."""
+    """Fuse projections along N; ``None`` when the parts cannot be fused.
+
+    Dense parts need equal width, device and dtype.  Quantized parts need the
+    same format and K/group (or block) and matching device/dtype per field,
+    and each part's N must be a multiple of every field's row granularity, so
+    that no packed zero-point word or scale block straddles two parts.
+    """
     import torch
 
     if not parts:
         return None
-    if all(isinstance(part, torch.Tensor) for part in parts):
-        first = parts[0]
-        if not all(
-            part.ndim == 2
-            and part.shape[1] == first.shape[1]
-            and part.device == first.device
-            and part.dtype == first.dtype
-            for part in parts
-        ):
+    kinds = {type(p) for p in parts}
+    if len(kinds) != 1:
+        return None
+    first = parts[0]
+    if isinstance(first, torch.Tensor):
+        key = (first.shape[1:] if first.ndim == 2 else None, first.device, first.dtype)
+        if any(p.ndim != 2 or (p.shape[1:], p.device, p.dtype) != key for p in parts):
             return None
-        return torch.cat(parts, dim=0).contiguous()
-    if all(isinstance(part, BlockScaledFP8Weight) for part in parts):
-        first = parts[0]
-        block_n, _ = first.block_size
-        # Every part must start on a scale-block boundary (N % 128 == 0).
-        if not all(
-            part.original_shape[1] == first.original_shape[1]
-            and part.block_size == first.block_size
-            and part.original_shape[0] % block_n == 0
-            and part.data.device == first.data.device
-            and part.scale_inv.device == first.scale_inv.device
-            and part.data.dtype == first.data.dtype
-            and part.scale_inv.dtype == first.scale_inv.dtype
-            for part in parts
-        ):
+        return torch.cat(list(parts), dim=0).contiguous()
+    if not isinstance(first, (PackedInt4Weight, BlockScaledFP8Weight)):
+        return None
+    fields = _storage(first)
+    granule = math.lcm(*fields.values())
+    if any(_static(p) != _static(first) or p.original_shape[0] % granule for p in parts):
+        return None
+    for name in fields:
+        key = _tensor_key(getattr(first, name))
+        if any(_tensor_key(getattr(p, name)) != key for p in parts):
             return None
-        return BlockScaledFP8Weight(
-            torch.cat([part.data for part in parts], dim=0).contiguous(),
-            torch.cat([part.scale_inv for part in parts], dim=0).contiguous(),
-            (sum(part.original_shape[0] for part in parts), first.original_shape[1]),
-            first.block_size,
-        )
-    if all(isinstance(part, PackedInt4Weight) for part in parts):
-        first = parts[0]
-        # Zero points pack 8 rows per word, so every part needs N % 8 == 0.
-        if not all(
-            part.original_shape[1] == first.original_shape[1]
-            and part.group_size == first.group_size
-            and part.original_shape[0] % 8 == 0
-            and part.packed.device == first.packed.device
-            and part.scale.device == first.scale.device
-            and part.zero_point.device == first.zero_point.device
-            and part.packed.dtype == first.packed.dtype
-            and part.scale.dtype == first.scale.dtype
-            and part.zero_point.dtype == first.zero_point.dtype
-            for part in parts
-        ):
-            return None
-        return PackedInt4Weight(
-            torch.cat([part.packed for part in parts], dim=0).contiguous(),
-            torch.cat([part.scale for part in parts], dim=0).contiguous(),
-            torch.cat([part.zero_point for part in parts], dim=0).contiguous(),
-            (sum(part.original_shape[0] for part in parts), first.original_shape[1]),
-            first.group_size,
-        )
-    return None
+    fused = {name: torch.cat([getattr(p, name) for p in parts], dim=0).contiguous() for name in fields}
+    rows = sum(p.original_shape[0] for p in parts)
+    return dataclasses.replace(first, **fused, original_shape=(rows, first.original_shape[1]))
 
 
 def split_linear_weight(fused, sizes: tuple[int, ...]):
-    """Views of a fused weight, one per output size (inverse of concatenation)."""
+    """Row views of a fused weight, one per output size (inverse of
+    ``concatenate_linear_weights``).  Quantized views share the fused storage."""
     import torch
 
     if isinstance(fused, torch.Tensor):
         return fused.split(sizes, dim=0)
-    if isinstance(fused, BlockScaledFP8Weight):
-        block_n, _ = fused.block_size
-        out = []
-        start = 0
-        for size in sizes:
-            out.append(
-                BlockScaledFP8Weight(
-                    fused.data.narrow(0, start, size),
-                    fused.scale_inv.narrow(0, start // block_n, size // block_n),
-                    (size, fused.original_shape[1]),
-                    fused.block_size,
-                )
-            )
-            start += size
-        return tuple(out)
-    if isinstance(fused, PackedInt4Weight):
-        out = []
-        start = 0
-        for size in sizes:
-            out.append(
-                PackedInt4Weight(
-                    fused.packed.narrow(0, start, size),
-                    fused.scale.narrow(0, start, size),
-                    fused.zero_point.narrow(0, start // 8, size // 8),
-                    (size, fused.original_shape[1]),
-                    fused.group_size,
-                )
-            )
-            start += size
-        return tuple(out)
-    raise TypeError(f"unsupported fused linear weight: {type(fused)!r}")
+    fields = _storage(fused)
+    views = []
+    row = 0
+    for size in sizes:
+        picked = {}
+        for name, per in fields.items():
+            if row % per or (size % per and row + size != fused.original_shape[0]):
+                raise ValueError(f"split at rows [{row}, {row + size}) is not aligned to {name}'s {per}-row entries")
+            picked[name] = getattr(fused, name).narrow(0, row // per, -(-size // per))
+        views.append(dataclasses.replace(fused, **picked, original_shape=(size, fused.original_shape[1])))
+        row += size
+    return tuple(views)

@@ -120,6 +120,13 @@ int hs_fp8_dequant(const uint8_t* data, int64_t ld_data,
                    void* out, int64_t ld_out, int out_dtype,
                    int N, int K, void* stream);
 
+/* Measurement aid, no counterpart in the reference: reads `bytes` bytes
+ * (a multiple of 16, 16-byte aligned) from src once with `blocks` workgroups
+ * of 256 threads and writes one word per workgroup to sink (sink_bytes >=
+ * 4 * blocks).  Its duration gives the streaming-read ceiling the decode
+ * GEMMs are compared against. */
+int hs_hbm_read_probe(const void* src, int64_t bytes, void* sink, int64_t sink_bytes, int blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,6 +55,27 @@ def test_c_validation_rejects_bad_args_without_launching():
     assert L.hs_int4_gemm(None, 0, None, 0, None, 0, 0, None, 0, None, 0, 0, 64, 256, 128, None, 0, None) == 0
 
 
+def test_operands_of_2gib_or_more_are_refused_not_truncated():
+    """Buffer resources address 32-bit byte ranges; the C ABI refuses larger
+    operands (HS_EUNSUPPORTED) before touching the device."""
+    L = _native.lib()
+    big_ld = 1 << 30  # X row stride in elements: the second row starts at 2 GiB
+    ws = 1 << 30
+    # X spans 2^31 bytes
+    assert L.hs_int4_gemm(16, big_ld, 16, 32, 16, 2, 0, 16, 2, 16, 64, 2, 64, 256, 128, 16, ws, None) == 3
+    assert L.hs_int4_gemm_silu_mul(16, big_ld, 16, 32, 16, 2, 0, 16, 2, 16, 64, 2, 64, 256, 128, 16, ws, None) == 3
+    assert L.hs_fp8_gemm(16, big_ld, 16, 256, 16, 2, 0, 16, 64, 2, 64, 256, 16, ws, None) == 3
+    # FP8 weight of 2^20 x 4096 bytes = 4 GiB
+    n, k = 1 << 20, 4096
+    assert L.hs_fp8_gemm(16, k, 16, k, 16, 32, 2, 16, n, 1, n, k, 16, ws, None) == 3
+    # INT4 packed rows with a 2^29-word stride
+    assert L.hs_int4_gemm(16, 256, 16, 1 << 29, 16, 2, 0, 16, 2, 16, 64, 1, 64, 256, 128, 16, ws, None) == 3
+    # output stride
+    assert L.hs_int4_gemm(16, 256, 16, 32, 16, 2, 0, 16, 2, 16, big_ld, 2, 64, 256, 128, 16, ws, None) == 3
+    # just under the limit is accepted by the check (missing workspace is reported instead)
+    assert L.hs_fp8_gemm(16, 256, 16, 256, 16, 2, 0, 16, 64, 1, 64, 256, None, 0, None) == 2
+
+
 def test_workspace_size_is_deterministic_and_covers_counters():
     L = _native.lib()
     a = L.hs_gemm_workspace_bytes(0, 1, 34816, 5120)
@@ -158,7 +179,55 @@ def test_concat_split_round_trip_int4_and_fp8():
     assert hs.concatenate_linear_weights([bad, f_parts[1]]) is None
 
 
+def test_split_views_share_storage_and_reject_misaligned_rows():
+    g = torch.Generator().manual_seed(1)
+    n = 48
+    w = PackedInt4Weight(
+        torch.randint(-(2**31), 2**31 - 1, (n, 32), generator=g, dtype=torch.int32),
+        torch.rand(n, 2, generator=g).to(torch.bfloat16),
+        torch.randint(-(2**31), 2**31 - 1, (n // 8, 2), generator=g, dtype=torch.int32),
+        (n, 256),
+    )
+    a, b = hs.split_linear_weight(w, (16, 32))
+    assert a.packed.data_ptr() == w.packed.data_ptr()
+    assert b.zero_point.data_ptr() == w.zero_point[2:].data_ptr() and b.zero_point.shape == (4, 2)
+    with pytest.raises(ValueError, match="zero_point"):
+        hs.split_linear_weight(w, (12, 36))
+    # a ragged FP8 tail keeps its partial scale row (ceil(N/128) rows per part)
+    f = BlockScaledFP8Weight(
+        torch.zeros(300, 128, dtype=torch.float8_e4m3fn), torch.rand(3, 1).to(torch.bfloat16), (300, 128)
+    )
+    head, tail = hs.split_linear_weight(f, (256, 44))
+    assert head.scale_inv.shape == (2, 1) and tail.scale_inv.shape == (1, 1)
+    assert torch.equal(tail.scale_inv, f.scale_inv[2:])
+    # mixed formats or dense + quantized do not fuse
+    assert hs.concatenate_linear_weights([w, f]) is None
+    assert hs.concatenate_linear_weights([torch.zeros(8, 256), w]) is None
+    assert hs.concatenate_linear_weights([]) is None
+
+
 def test_linear_dispatch_dense_branch():
     w = torch.randn(5, 7)
     x = torch.randn(3, 7)
     torch.testing.assert_close(hs.linear(x, w), x @ w.T)
+
+
+def test_custom_ops_are_registered_with_fake_implementations():
+    """torch.compile sees opaque ops (hydraserve_amd/ops.py); their fake
+    implementations give the output shape and dtype without a device."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    for name in ("int4_gemm", "fp8_gemm", "int4_gate_up_silu_mul"):
+        assert hasattr(torch.ops.hydraserve_amd, name)
+    with FakeTensorMode():
+        x = torch.empty(3, 256, dtype=torch.bfloat16)
+        packed = torch.empty(64, 32, dtype=torch.int32)
+        scale = torch.empty(64, 2, dtype=torch.bfloat16)
+        zero = torch.empty(8, 2, dtype=torch.int32)
+        y = torch.ops.hydraserve_amd.int4_gemm(x, packed, scale, zero, 64, 256, 128)
+        assert y.shape == (3, 64) and y.dtype == torch.bfloat16
+        y = torch.ops.hydraserve_amd.int4_gate_up_silu_mul(x, packed, scale, zero, 64, 256, 128)
+        assert y.shape == (3, 32)
+        data = torch.empty(64, 256, dtype=torch.uint8)
+        y = torch.ops.hydraserve_amd.fp8_gemm(x, data, torch.empty(1, 2), 64, 256)
+        assert y.shape == (3, 64) and y.dtype == torch.bfloat16

@@ -489,9 +489,17 @@ def test_fp8_streams_host_resident_weight():
 
 
 # ---------------------------------------------------------------- BASELINE shapes
-def _sampled_columns(rng, n, count=48):
-    cols = rng.choice(n, size=count, replace=False)
-    return np.sort(np.concatenate([cols, [0, n - 1]]))
+def _tile_columns(n, seed=0):
+    """Output columns checked at full size: one in every 16-row weight block
+    (the smallest tile any kernel uses; the position inside the block rotates
+    over all 16 lanes), plus the first and last column of every 256-wide
+    block, the widest tile.  Every tile of every kernel, including tiles whose
+    K range is split across workgroups, therefore has checked columns at both
+    of its edges or inside it."""
+    blocks = np.arange((n + 15) // 16)
+    inner = np.minimum(16 * blocks + (blocks * 7 + seed) % 16, n - 1)
+    edges = np.concatenate([np.arange(0, n, 256), np.minimum(np.arange(255, n + 255, 256), n - 1)])
+    return np.unique(np.concatenate([inner, edges]))
 
 
 CONFIG4_SHAPES = [(10240, 5120), (5120, 8192), (12288, 5120)]  # qkv, o_proj, GDN in_proj (N, K)
@@ -499,12 +507,14 @@ CONFIG4_SHAPES = [(10240, 5120), (5120, 8192), (12288, 5120)]  # qkv, o_proj, GD
 
 @pytest.mark.parametrize(
     "m,n,k",
-    [(m, n, k) for m in (1, 4, 16, 64, 128, 512, 2048) for n, k in ((34816, 5120), (5120, 17408))]
+    [(8, 4096, 4096)]  # config 0
+    + [(m, n, k) for m in (1, 4, 16, 64, 128, 512, 1024, 2048) for n, k in ((34816, 5120), (5120, 17408))]
     + [(m, n, k) for m in (64, 1024) for n, k in CONFIG4_SHAPES],
 )
 def test_int4_baseline_shapes_sampled_oracle(m, n, k):
-    """Full-size configs 1, 2 and 4: uniform random packed words (uniform
-    nibbles) on the GPU; the oracle recomputes 50 sampled output columns."""
+    """Full-size configs 0, 1, 2 and 4 (gate_up and down also at M=1024, the
+    config-4 layer): uniform random packed words (uniform nibbles) on the GPU;
+    the oracle recomputes the columns of _tile_columns (every tile covered)."""
     dev = _cuda()
     g = torch.Generator(device="cpu").manual_seed(m + n)
     kw, groups = k // 8, k // 128
@@ -514,8 +524,7 @@ def test_int4_baseline_shapes_sampled_oracle(m, n, k):
     x = torch.randn(m, k, generator=g).to(torch.bfloat16)
     w = PackedInt4Weight(packed.to(dev), scale.to(dev), zero.to(dev), (n, k))
     y = hs.awq_linear(x.to(dev), w).cpu()
-    rng = np.random.default_rng(m)
-    cols = _sampled_columns(rng, n)
+    cols = _tile_columns(n, m)
     zp_rows = qo.unpack_zero_points(zero.numpy(), n)[cols]
     q = qo.unpack_int4_rows(packed.numpy()[cols], k).astype(np.int32)
     s = scale.float().numpy()[cols]
@@ -536,8 +545,7 @@ def test_fp8_baseline_shapes_sampled_oracle(m, n, k):
     x = torch.randn(m, k, generator=g).to(torch.bfloat16)
     w = BlockScaledFP8Weight(data.to(dev).view(torch.float8_e4m3fn), scale.to(dev), (n, k))
     y = hs.fp8_linear(x.to(dev), w).cpu()
-    rng = np.random.default_rng(m)
-    cols = _sampled_columns(rng, n)
+    cols = _tile_columns(n, m)
     wd = qo.decode_e4m3fn(data.numpy()[cols]) * scale.numpy()[(cols // 128)][:, np.arange(k) // 128]
     ref = qo.gemm_f64(x.float().numpy(), wd.astype(np.float32))
     assert_gemm_close(y[:, cols], ref, what=f"m={m} {n}x{k}")

@@ -143,3 +143,55 @@ def _check_fused(m, n, k, scale_dtype):
     # output's magnitude: the absolute bar scales with it
     mag = max(1.0, unfused.float().abs().max().item())
     torch.testing.assert_close(out.float(), unfused.float(), atol=2e-2 * mag, rtol=2e-2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 8, 16, 64, 2048])
+def test_fused_gate_up_silu_mul_full_shape(m):
+    """The benchmarked shape, gate_up 5120 -> 34816: at 1..16 rows the
+    block-major kernel's largest row partitions and the row-partitioned
+    kernel's widest SiLU instance, at 64 the streaming kernel's two-column-block
+    store, at 2048 the prefill SiLU instance.  The oracle recomputes gate and up
+    for the output columns of test_gemm_gpu._tile_columns (every tile)."""
+    if not torch.cuda.is_available():
+        pytest.skip("needs a ROCm GPU")
+    from hydraserve_amd.kernels import awq_gate_up_silu_mul
+
+    from . import test_gemm_gpu as tg
+
+    dev = torch.device("cuda", 0)
+    n, k = 34816, 5120
+    half = n // 2
+    g = torch.Generator(device="cpu").manual_seed(900 + m)
+    groups = k // 128
+    packed = torch.randint(-(2**31), 2**31 - 1, (n, k // 8), generator=g, dtype=torch.int32)
+    zero = torch.randint(-(2**31), 2**31 - 1, (n // 8, groups), generator=g, dtype=torch.int32)
+    scale = (torch.rand(n, groups, generator=g) * 9e-3 + 1e-3).to(torch.bfloat16)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = PackedInt4Weight(packed.to(dev), scale.to(dev), zero.to(dev), (n, k))
+    wi = interleave_gate_up(w)
+    from hydraserve_amd import _native
+
+    assert _native.int4_gemm_silu_mul(x.to(dev), wi.packed, wi.scale, wi.zero_point, n, k, 128) is not None
+    out = awq_gate_up_silu_mul(x.to(dev), wi).cpu()
+    assert out.shape == (m, half)
+    cols = tg._tile_columns(half, m)
+    rows = np.concatenate([cols, half + cols])
+    zp = qo.unpack_zero_points(zero.numpy(), n)[rows].astype(np.int32)
+    q = qo.unpack_int4_rows(packed.numpy()[rows], k).astype(np.int32)
+    s = scale.float().numpy()[rows]
+    gi = np.arange(k) // 128
+    xf = x.float().numpy()
+    w_exact = (q - zp[:, gi]).astype(np.float64) * s[:, gi]
+    wd = qo.bf16_bits_to_f32(qo.f32_to_bf16_bits((q - zp[:, gi]).astype(np.float32) * s[:, gi]))
+    y = qo.gemm_f64(xf, wd)
+    y_exact = xf.astype(np.float64) @ w_exact.T
+
+    def act(yy):
+        gu = qo.bf16_bits_to_f32(qo.f32_to_bf16_bits(np.asarray(yy, dtype=np.float32))).astype(np.float64)
+        gate, up = gu[:, : len(cols)], gu[:, len(cols) :]
+        return gate / (1.0 + np.exp(-gate)) * up
+
+    ref = act(y).view(tg.RefArray)
+    ref.exact = act(y_exact)
+    tg.assert_gemm_close(out[:, cols], ref, what=f"fused silu_mul full shape M={m}")
