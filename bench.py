@@ -251,12 +251,10 @@ def hbm_ceiling(torch, dev, nbytes=4 << 30):
     return {"GBps": round(best[0], 1), "bytes": nbytes, "workgroups": best[1]}
 
 
-# Every BASELINE config as (config, kind, shape, M list); configs 1 and 4 share
-# gate_up/down at M=64.
+# Every BASELINE config besides the headline's config 1 as (config, kind,
+# shape, M list); config 4 takes gate_up/down at M=64 from config 1.
 ALL_CONFIGS = [
     ("c0", "int4", "c0", [8]),
-    ("c1", "int4", "gate_up", [1, 4, 16, 64]),
-    ("c1", "int4", "down", [1, 4, 16, 64]),
     ("c2", "int4", "gate_up", [512, 2048]),
     ("c2", "int4", "down", [512, 2048]),
     ("c3", "fp8", "gate_up", [1, 16, 256, 2048]),
@@ -269,9 +267,10 @@ ALL_CONFIGS = [
 ]
 
 
-def measure_all(torch, gen, dev):
+def measure_all(torch, gen, dev, headline):
     """One timed entry per (config, shape, M): graphs of back-to-back launches
-    over rotated weight copies, HIP events around the replays."""
+    over rotated weight copies, HIP events around the replays.  `headline`:
+    the config-1 entries already measured."""
     out = []
     for cfg, kind, name, m_list in ALL_CONFIGS:
         n, k = SHAPES[name]
@@ -292,7 +291,7 @@ def measure_all(torch, gen, dev):
         torch.cuda.empty_cache()
     # config 4: summed latency of one decoder layer's projections
     layer = {}
-    for r in out:
+    for r in headline + out:
         if r["kind"] == "int4" and r["shape"] in ("qkv", "o_proj", "gdn_in", "gate_up", "down") and r["M"] in (64, 1024):
             layer.setdefault(r["M"], []).append(r["us"])
     c4 = {str(m): {"us": round(sum(v), 2), "linears": len(v)} for m, v in sorted(layer.items())}
@@ -430,7 +429,7 @@ def main():
     }
 
     if not args.headline_only:
-        entries, c4 = measure_all(torch, gen, dev)
+        entries, c4 = measure_all(torch, gen, dev, result["per_shape"])
         result["per_shape"] += entries
         result["config4_layer"] = c4
         prefill = [r for r in entries if r["bound"] == "mfma"]

@@ -30,6 +30,7 @@ SIGNATURES = {
     "hs_error_string": (ctypes.c_char_p, [_I]),
     "hs_gemm_workspace_bytes": (_I64, [_I, _I, _I, _I]),
     "hs_int4_gemm": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _I64, _P]),
+    "hs_int4_gemm_noalloc": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
     "hs_int4_gemm_silu_mul": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _I64, _P]),
     "hs_fp8_gemm": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _I, _I, _I, _P, _I64, _P]),
     "hs_int4_dequant": (_I, [_P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),

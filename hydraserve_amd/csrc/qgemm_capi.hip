@@ -390,6 +390,60 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   return hip_code(e);
 }
 
+// ---- fixed scratch for callers that cannot allocate (hs_int4_gemm_noalloc) --
+// One file-scope device array per GPU holds the split-K workspace: arrival
+// counters first (which every kernel returns to zero when it finishes), then
+// the partial tiles.  Host code never uses the array's name as an address:
+// the device address comes from hipGetSymbolAddress, once per device, with
+// that device current.
+constexpr int64_t kScratchBytes = int64_t(40) << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+struct ScratchSlot {
+  void* ptr = nullptr;
+  bool cleared = false;
+};
+ScratchSlot g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+__global__ void clear_words_kernel(uint32_t* p, int64_t words) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words; i += stride) p[i] = 0u;
+}
+
+// Device address of this device's scratch array; on the first call per device
+// the counter block is cleared with a fill kernel on `stream` (no memset node,
+// so the call may be captured).  The clear is repeated until it has run on a
+// stream that was not capturing, so a captured-but-never-replayed first call
+// cannot leave the counters uncleared.
+int scratch_for_device(hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_code(e);
+  if (dev < 0 || dev >= kMaxDevices) return HS_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchSlot& slot = g_scratch[dev];
+  if (slot.ptr == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_code(e);
+    if (ptr == nullptr) return HS_EHIP + static_cast<int>(hipErrorInvalidSymbol);
+    slot.ptr = ptr;
+  }
+  if (!slot.cleared) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return hip_code(e);
+    hipLaunchKernelGGL(clear_words_kernel, dim3(256), dim3(256), 0, stream, static_cast<uint32_t*>(slot.ptr),
+                       kCounterBytes / 4);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_code(e);
+    slot.cleared = cs == hipStreamCaptureStatusNone;
+  }
+  *out = slot.ptr;
+  return HS_OK;
+}
+
 }  // namespace
 }  // namespace hsq
 
@@ -403,6 +457,7 @@ const char* hs_error_string(int code) {
     case HS_EINVAL: return "invalid argument (shape, stride, pointer or dtype code)";
     case HS_EWORKSPACE: return "workspace missing or smaller than hs_gemm_workspace_bytes()";
     case HS_EUNSUPPORTED: return "unsupported configuration";
+    case HS_ESCRATCH: return "problem needs more split-K workspace than the fixed scratch array holds (hs_int4_gemm_noalloc)";
     default: break;
   }
   if (code >= HS_EHIP) return hipGetErrorString(static_cast<hipError_t>(code - HS_EHIP));
@@ -454,6 +509,27 @@ int hs_int4_gemm(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_p
   a.wvec = hsq::aligned16(packed) && (ld_packed % 4 == 0);
   a.tune = hsq::tuning().tune;
   return hsq::run_gemm(hsq::W_INT4, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int hs_int4_gemm_noalloc(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,
+                         int64_t ld_scale, int scale_dtype, const int32_t* zero_point, int64_t ld_zero, void* y,
+                         int64_t ldy, int M, int N, int K, int group, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return HS_EINVAL;
+  if (group != 128) return HS_EUNSUPPORTED;
+  if (M == 0 || N == 0) return HS_OK;
+  // Argument checks first, so a rejected call touches no device state.
+  if (K == 0) return HS_EUNSUPPORTED;
+  if (x == nullptr || packed == nullptr || scale == nullptr || zero_point == nullptr || y == nullptr) return HS_EINVAL;
+  if (ldx < K || ld_packed < (K + 7) / 8 || ld_scale < (K + 127) / 128 || ld_zero < (K + 127) / 128 || ldy < N)
+    return HS_EINVAL;
+  if (!hsq::valid_dt(scale_dtype)) return HS_EINVAL;
+  void* ws = nullptr;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rc0 = hsq::scratch_for_device(s, &ws);
+  if (rc0 != HS_OK) return rc0;
+  const int rc = hs_int4_gemm(x, ldx, packed, ld_packed, scale, ld_scale, scale_dtype, zero_point, ld_zero, y, ldy, M,
+                              N, K, group, ws, hsq::kScratchBytes, stream);
+  return rc == HS_EWORKSPACE ? HS_ESCRATCH : rc;
 }
 
 int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,

@@ -33,6 +33,7 @@ extern "C" {
 #define HS_EINVAL 1        /* bad shape, stride, pointer or enum */
 #define HS_EWORKSPACE 2    /* workspace missing or smaller than hs_gemm_workspace_bytes() */
 #define HS_EUNSUPPORTED 3  /* valid request this library does not implement (e.g. group != 128) */
+#define HS_ESCRATCH 4      /* hs_int4_gemm_noalloc: the problem needs more workspace than its fixed scratch */
 #define HS_EHIP 1000       /* HS_EHIP + hipError_t from a HIP runtime call */
 
 /* scale / output dtype codes */
@@ -70,6 +71,25 @@ int hs_int4_gemm(const void* x, int64_t ldx,
                  int M, int N, int K, int group,
                  void* workspace, int64_t workspace_bytes,
                  void* stream);
+
+/* hs_int4_gemm without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture that may not call
+ * hipMalloc, tight serving loops, harnesses that forbid allocation).  No
+ * counterpart in the reference.  The split-K workspace is a fixed device
+ * array inside the library, one per GPU, of 40 MiB (held from library load
+ * until the process ends): problems whose
+ * plan needs more return HS_ESCRATCH (at the BASELINE shapes: every M up to
+ * 64; prefill M >= 129 does not fit).  The call allocates nothing.  All calls on one GPU
+ * share that GPU's array, so calls that overlap in time on one GPU (two
+ * streams, two threads) race; serialise them.  Results are those of
+ * hs_int4_gemm. */
+int hs_int4_gemm_noalloc(const void* x, int64_t ldx,
+                         const int32_t* packed, int64_t ld_packed,
+                         const void* scale, int64_t ld_scale, int scale_dtype,
+                         const int32_t* zero_point, int64_t ld_zero,
+                         void* y, int64_t ldy,
+                         int M, int N, int K, int group,
+                         void* stream);
 
 /* The MLP's gate_up projection with SiLU-and-mul fused into the GEMM's store:
  * out[M, N/2] = silu(gate) * up, gate and up being the bf16 outputs of

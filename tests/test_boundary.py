@@ -231,3 +231,14 @@ def test_custom_ops_are_registered_with_fake_implementations():
         data = torch.empty(64, 256, dtype=torch.uint8)
         y = torch.ops.hydraserve_amd.fp8_gemm(x, data, torch.empty(1, 2), 64, 256)
         assert y.shape == (3, 64) and y.dtype == torch.bfloat16
+
+
+def test_noalloc_entry_point_validates_before_touching_the_device():
+    L = _native.lib()
+    # group != 128, null pointers, short strides, bad dtype: rejected on the host
+    assert L.hs_int4_gemm_noalloc(16, 256, 16, 32, 16, 2, 0, 16, 2, 16, 64, 1, 64, 256, 64, None) == 3
+    assert L.hs_int4_gemm_noalloc(None, 256, None, 32, None, 2, 0, None, 2, None, 64, 1, 64, 256, 128, None) == 1
+    assert L.hs_int4_gemm_noalloc(16, 100, 16, 32, 16, 2, 0, 16, 2, 16, 64, 1, 64, 256, 128, None) == 1
+    assert L.hs_int4_gemm_noalloc(16, 256, 16, 32, 16, 2, 9, 16, 2, 16, 64, 1, 64, 256, 128, None) == 1
+    assert L.hs_int4_gemm_noalloc(None, 0, None, 0, None, 0, 0, None, 0, None, 0, 0, 64, 256, 128, None) == 0
+    assert b"scratch" in L.hs_error_string(4)
