@@ -47,8 +47,18 @@ def build(verbose: bool = False) -> Path:
     hipcc = _hipcc()
     BUILD_DIR.mkdir(exist_ok=True)
 
+    # HS_BUILD_INCREMENTAL=1 (development only): skip sources whose object is
+    # newer than the source and every header; build() itself always compiles all.
+    incremental = os.environ.get("HS_BUILD_INCREMENTAL") == "1"
+    headers = [*CSRC.glob("*.h"), PKG.parent / "include" / "hydraserve_amd.h"]
+    newest_header = max(h.stat().st_mtime for h in headers)
+
     def compile_one(src: str) -> Path:
         obj = BUILD_DIR / (Path(src).stem + ".o")
+        if incremental and obj.exists():
+            t = obj.stat().st_mtime
+            if t > (CSRC / src).stat().st_mtime and t > newest_header:
+                return obj
         cmd = [hipcc, *_flags(), "-c", str(CSRC / src), "-o", str(obj)]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
