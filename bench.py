@@ -298,6 +298,56 @@ def measure_all(torch, gen, dev, headline):
     return out, c4
 
 
+def host_stream(torch, gen, dev, reps=3):
+    """FP8 gate_up with its weight in page-locked host memory (the loader's
+    offload case, hydraserve/model/runtime.py:182-236): the reference's
+    sequence (stage the whole weight, then the GEMM; fp8.py:32-41) against the
+    slab stream that overlaps the copies with the GEMMs.  PCIe-inclusive,
+    eager, events on the current stream; median of `reps`."""
+    import statistics
+
+    import hydraserve_amd as hs
+    from hydraserve_amd.kernels import pin_fp8_weight
+    from hydraserve_amd.model.weights import BlockScaledFP8Weight
+
+    n, k = GATE_UP
+    w_dev = make_fp8(torch, n, k, 1, gen, dev)[0]
+    host = pin_fp8_weight(BlockScaledFP8Weight(w_dev.data.cpu(), w_dev.scale_inv.cpu(), (n, k)))
+    del w_dev
+    out = []
+    for m in (16, 2048):
+        x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
+
+        def serial():
+            staged = BlockScaledFP8Weight(host.data.to(dev, non_blocking=True), host.scale_inv.to(dev, non_blocking=True), (n, k))
+            return hs.fp8_linear(x, staged)
+
+        def overlapped():
+            return hs.fp8_linear(x, host)
+
+        res = {}
+        for name, fn in (("serial", serial), ("overlapped", overlapped)):
+            fn()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(reps):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                fn()
+                b.record()
+                torch.cuda.synchronize()
+                ts.append(a.elapsed_time(b) * 1e3)
+            res[name] = statistics.median(ts)
+        r = {"kind": "fp8", "shape": "gate_up (host-resident, pinned)", "M": m, "N": n, "K": k,
+             "serial_us": round(res["serial"], 1), "overlapped_us": round(res["overlapped"], 1),
+             "pcie_inclusive_weight_GBps": round(fp8_bytes(n, k) / (res["overlapped"] * 1e-6) / 1e9, 1)}
+        print(json.dumps(r), file=sys.stderr, flush=True)
+        out.append(r)
+    del host
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -445,6 +495,8 @@ def main():
             "flops_per_launch": 2 * dom_p["M"] * dom_p["N"] * dom_p["K"],
             "us_per_launch": dom_p["us"],
         }
+
+        result["fp8_host_stream"] = host_stream(torch, gen, dev)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(16)

@@ -189,6 +189,29 @@ def fp8_gemm(x, data_u8, scale_inv, n: int, k: int):
     return y
 
 
+def fp8_gemm_into(x, data_u8, scale_inv, y, col0: int, n: int, k: int) -> None:
+    """Y[:, col0:col0+n] = x . W^T for an FP8 row slab W [n, K] (its own scale
+    rows), written in place into a wider bf16 output y (row stride y.stride(0))."""
+    import torch
+
+    m = x.shape[0]
+    if m == 0 or n == 0:
+        return
+    L = lib()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    need = L.hs_gemm_workspace_bytes(HS_KIND_FP8, m, n, k)
+    ws = workspaces.get(x.device, stream, need)
+    check(
+        L.hs_fp8_gemm(
+            x.data_ptr(), x.stride(0), data_u8.data_ptr(), data_u8.stride(0),
+            scale_inv.data_ptr(), scale_inv.stride(0), dtype_code(scale_inv.dtype),
+            y.data_ptr() + col0 * y.element_size(), y.stride(0), m, n, k,
+            ws.data_ptr(), ws.numel(), stream,
+        ),
+        "hs_fp8_gemm",
+    )
+
+
 def int4_dequant(packed, scale, zero_point, n: int, k: int, group: int, out_dtype):
     import torch
 

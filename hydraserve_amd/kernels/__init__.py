@@ -2,6 +2,7 @@
 
 from .awq import awq_linear, dequantize_int4_weight
 from .fp8 import dequantize_fp8_weight, fp8_linear
+from .fp8_stream import pin_fp8_weight
 from .mlp import awq_gate_up_silu_mul, deinterleave_gate_up, interleave_gate_up, silu_and_mul
 
 __all__ = [
@@ -9,6 +10,7 @@ __all__ = [
     "dequantize_int4_weight",
     "fp8_linear",
     "dequantize_fp8_weight",
+    "pin_fp8_weight",
     "interleave_gate_up",
     "deinterleave_gate_up",
     "silu_and_mul",

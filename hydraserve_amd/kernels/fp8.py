@@ -2,7 +2,8 @@
 
 Drop-in for hydraserve/kernels/fp8.py: same function names, arguments,
 validation order, messages and exception types (fp8.py:24-62), including the
-staging of host-resident weights onto the activation's GPU (fp8.py:32-41).
+staging of host-resident weights onto the activation's GPU (fp8.py:32-41);
+page-locked host weights take the overlapped slab stream of fp8_stream.py.
 Execution is the HIP kernels of libhydraserve_amd.so; unlike the reference
 there is no CPU execution branch (fp8.py:51-53).
 """
@@ -11,6 +12,7 @@ from __future__ import annotations
 
 from .. import _native
 from ._device import device_guard, require_gpu
+from .fp8_stream import PREFILL_ROWS, is_pinned_weight, streamed_fp8_gemm
 
 
 def _check_scale_grid(weight) -> None:
@@ -48,6 +50,25 @@ def dequantize_fp8_weight(weight, *, dtype=None):
         return _native.fp8_dequant(data, weight.scale_inv, n, k, out_dtype)
 
 
+def _streamed(hidden, weight):
+    import torch
+
+    _check_scale_grid(weight)
+    n, k = weight.original_shape
+    data = _as_bytes(weight.data)
+    if tuple(data.shape) != (n, k) or not (data.is_contiguous() and weight.scale_inv.is_contiguous()):
+        raise ValueError("FP8 data and scales must be contiguous tensors of the weight's shape")
+    flattened = hidden.reshape(-1, k).contiguous()
+    if flattened.dtype != torch.bfloat16:
+        raise TypeError("hydraserve_amd quantized GEMMs take bfloat16 activations")
+    _native.dtype_code(weight.scale_inv.dtype)
+    shape = hidden.shape[:-1] + (n,)
+    if k == 0:
+        return torch.zeros(shape, device=hidden.device, dtype=hidden.dtype)
+    with device_guard(hidden.device):
+        return streamed_fp8_gemm(flattened, weight).reshape(shape)
+
+
 def fp8_linear(hidden, weight):
     """Multiply BF16 activations by block-scaled E4M3 weights."""
     import torch
@@ -59,6 +80,10 @@ def fp8_linear(hidden, weight):
     if hidden.device != weight.data.device:
         if not hidden.is_cuda or weight.data.device.type != "cpu":
             raise ValueError("unsupported activation/FP8 weight device placement")
+        rows = hidden.numel() // max(hidden.shape[-1], 1)
+        if is_pinned_weight(weight) and rows >= PREFILL_ROWS and not torch.compiler.is_compiling():
+            # page-locked host weight: slab copies overlapped with slab GEMMs
+            return _streamed(hidden, weight)
         staged = type(weight)(
             weight.data.to(hidden.device, non_blocking=True).contiguous(),
             weight.scale_inv.to(hidden.device, non_blocking=True).contiguous(),
