@@ -11,6 +11,7 @@ All compute runs in libhydraserve_amd.so (hand-written HIP for gfx950).
 
 from . import ops  # noqa: F401  (registers the torch.library custom ops)
 from .kernels import awq_linear, dequantize_fp8_weight, dequantize_int4_weight, fp8_linear
+from .model.checkpoint import CheckpointReader, load_linear_weights, read_linear
 from .model.linear import concatenate_linear_weights, linear, split_linear_weight
 from .model.weights import BlockScaledFP8Weight, PackedInt4Weight
 
@@ -24,4 +25,7 @@ __all__ = [
     "linear",
     "concatenate_linear_weights",
     "split_linear_weight",
+    "CheckpointReader",
+    "load_linear_weights",
+    "read_linear",
 ]
