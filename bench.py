@@ -90,7 +90,11 @@ def make_fp8(torch, n, k, copies, gen, dev):
 # `bench.py --profile KIND:SHAPE:M` (KiB per dispatch), scaled by what the same
 # counters read for a 512 MiB copy: FETCH x2.0, WRITE x1.0.  Kept beside the
 # summaries under profiles/; shapes not listed report null.
-PMC_TRAFFIC_KIB = {("int4", "gate_up", 64): (69799.2, 28954.0)}
+PMC_TRAFFIC_KIB = {
+    ("int4", "gate_up", 64): (69799.2, 28954.0),
+    ("int4", "down", 64): (36461.5, 9866.2),
+    ("int4", "down", 16): (26201.5, 1452.5),
+}
 FETCH_CAL, WRITE_CAL = 2.0, 1.0
 
 
@@ -513,6 +517,12 @@ SHAPES = {"gate_up": GATE_UP, "down": DOWN, "c0": C0, "qkv": QKV, "o_proj": O_PR
 COPY_CAL_BYTES = 512 << 20
 
 
+def _native_probe(src, sink):
+    from hydraserve_amd import _native
+
+    _native.hbm_read_probe(src, sink, 2048)
+
+
 def profile(torch, gen, dev, spec, launches):
     """One GEMM launched eagerly `launches` times over rotated weight copies, then a
     512 MiB device-to-device copy launched 4 times.  Under rocprofv3 --pmc the copy's
@@ -543,6 +553,11 @@ def profile(torch, gen, dev, spec, launches):
     dst = torch.empty_like(src)
     for _ in range(4):
         dst.copy_(src)
+    # a plain streaming read of the same 512 MiB (hs_hbm_read_probe): reads
+    # only, so FETCH_SIZE calibrates against known bytes without write traffic
+    sink = torch.empty(4096, dtype=torch.int32, device=dev)
+    for _ in range(4):
+        _native_probe(src, sink)
     torch.cuda.synchronize()
     print(json.dumps({"profile": spec, "launches": launches, "weight_bytes_per_launch": c.wbytes,
                       "copy_bytes_per_launch": COPY_CAL_BYTES}), flush=True)
