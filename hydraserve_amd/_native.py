@@ -33,6 +33,8 @@ SIGNATURES = {
     "hs_int4_gemm_noalloc": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
     "hs_int4_gemm_silu_mul": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _I64, _P]),
     "hs_fp8_gemm": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _I, _I, _I, _P, _I64, _P]),
+    "hs_int4_gemm_tiled": (_I, [_P, _I64, _P, _I64, _P, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _I64, _P]),
+    "hs_fp8_gemm_tiled": (_I, [_P, _I64, _P, _I64, _P, _P, _I64, _I, _P, _I64, _I, _I, _I, _P, _I64, _P]),
     "hs_int4_dequant": (_I, [_P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
     "hs_fp8_dequant": (_I, [_P, _I64, _P, _I64, _I, _P, _I64, _I, _I, _I, _P]),
     "hs_hbm_read_probe": (_I, [_P, _I64, _P, _I64, _I, _P]),
@@ -115,8 +117,9 @@ class _Workspaces:
 workspaces = _Workspaces()
 
 
-def int4_gemm(x, packed, scale, zero_point, n: int, k: int, group: int):
-    """Y[M, N] (bf16) for a contiguous bf16 x [M, K] on the current stream."""
+def int4_gemm(x, packed, scale, zero_point, n: int, k: int, group: int, tiles=None):
+    """Y[M, N] (bf16) for a contiguous bf16 x [M, K] on the current stream
+    (``tiles``: the load-time tiled copy of packed, kernels/tiles.py)."""
     import torch
 
     m = x.shape[0]
@@ -127,6 +130,18 @@ def int4_gemm(x, packed, scale, zero_point, n: int, k: int, group: int):
     stream = torch.cuda.current_stream(x.device).cuda_stream
     need = L.hs_gemm_workspace_bytes(HS_KIND_INT4, m, n, k)
     ws = workspaces.get(x.device, stream, need)
+    if tiles is not None:
+        check(
+            L.hs_int4_gemm_tiled(
+                x.data_ptr(), x.stride(0), packed.data_ptr(), packed.stride(0), tiles.data_ptr(),
+                scale.data_ptr(), scale.stride(0), dtype_code(scale.dtype),
+                zero_point.data_ptr(), zero_point.stride(0),
+                y.data_ptr(), y.stride(0), m, n, k, group,
+                ws.data_ptr(), ws.numel(), stream,
+            ),
+            "hs_int4_gemm_tiled",
+        )
+        return y
     check(
         L.hs_int4_gemm(
             x.data_ptr(), x.stride(0), packed.data_ptr(), packed.stride(0),
@@ -166,7 +181,7 @@ def int4_gemm_silu_mul(x, packed, scale, zero_point, n: int, k: int, group: int)
     return y
 
 
-def fp8_gemm(x, data_u8, scale_inv, n: int, k: int):
+def fp8_gemm(x, data_u8, scale_inv, n: int, k: int, tiles=None):
     import torch
 
     m = x.shape[0]
@@ -177,6 +192,17 @@ def fp8_gemm(x, data_u8, scale_inv, n: int, k: int):
     stream = torch.cuda.current_stream(x.device).cuda_stream
     need = L.hs_gemm_workspace_bytes(HS_KIND_FP8, m, n, k)
     ws = workspaces.get(x.device, stream, need)
+    if tiles is not None:
+        check(
+            L.hs_fp8_gemm_tiled(
+                x.data_ptr(), x.stride(0), data_u8.data_ptr(), data_u8.stride(0), tiles.data_ptr(),
+                scale_inv.data_ptr(), scale_inv.stride(0), dtype_code(scale_inv.dtype),
+                y.data_ptr(), y.stride(0), m, n, k,
+                ws.data_ptr(), ws.numel(), stream,
+            ),
+            "hs_fp8_gemm_tiled",
+        )
+        return y
     check(
         L.hs_fp8_gemm(
             x.data_ptr(), x.stride(0), data_u8.data_ptr(), data_u8.stride(0),

@@ -347,6 +347,8 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   if (!use_skinny && !tn.gemv_off && a.M <= 16 && !gemv_narrow) {
     const int P = device_cus() * (tn.gemv_wg > 0 ? tn.gemv_wg : 1);
     int kw = 0, rows_max = 0;
+    // the tiled weight copy (if any) is read by this kernel only
+    if (a.wtiles != nullptr && !gemv_ok(a, wt, P, tn.gemv_kw > 0 ? tn.gemv_kw : 8, &kw, &rows_max)) a.wtiles = nullptr;
     if (gemv_ok(a, wt, P, tn.gemv_kw > 0 ? tn.gemv_kw : 8, &kw, &rows_max)) {
       a.P = P;
       a.T = a.K / 128;
@@ -354,6 +356,7 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
       return hip_code(launch_gemv(wt, a, kw, stream));
     }
   }
+  a.wtiles = nullptr;
   if (!use_skinny && !tn.rows_off && a.M <= (tn.rows_ms2_off ? 16 : 32)) {
     const int P = device_cus() * (tn.rows_wg > 0 ? tn.rows_wg : 1);
     int nblk = 0, ms = 1;
@@ -480,9 +483,10 @@ int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
   return best;
 }
 
-int hs_int4_gemm(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,
-                 int64_t ld_scale, int scale_dtype, const int32_t* zero_point, int64_t ld_zero, void* y, int64_t ldy,
-                 int M, int N, int K, int group, void* workspace, int64_t workspace_bytes, void* stream) {
+static int int4_gemm_impl(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,
+                          int64_t ld_scale, int scale_dtype, const int32_t* zero_point, int64_t ld_zero,
+                          const int32_t* tiles, void* y, int64_t ldy, int M, int N, int K, int group, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
   if (M < 0 || N < 0 || K < 0) return HS_EINVAL;
   if (group != 128) return HS_EUNSUPPORTED;
   if (M == 0 || N == 0) return HS_OK;
@@ -508,7 +512,24 @@ int hs_int4_gemm(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_p
   a.K = K;
   a.wvec = hsq::aligned16(packed) && (ld_packed % 4 == 0);
   a.tune = hsq::tuning().tune;
+  a.wtiles = tiles != nullptr && hsq::aligned16(tiles) && K % 128 == 0 && N % 16 == 0 ? tiles : nullptr;
   return hsq::run_gemm(hsq::W_INT4, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int hs_int4_gemm(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,
+                 int64_t ld_scale, int scale_dtype, const int32_t* zero_point, int64_t ld_zero, void* y, int64_t ldy,
+                 int M, int N, int K, int group, void* workspace, int64_t workspace_bytes, void* stream) {
+  return int4_gemm_impl(x, ldx, packed, ld_packed, scale, ld_scale, scale_dtype, zero_point, ld_zero, nullptr, y, ldy, M,
+                        N, K, group, workspace, workspace_bytes, stream);
+}
+
+int hs_int4_gemm_tiled(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const int32_t* tiles,
+                       const void* scale, int64_t ld_scale, int scale_dtype, const int32_t* zero_point,
+                       int64_t ld_zero, void* y, int64_t ldy, int M, int N, int K, int group, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+  if (tiles == nullptr) return HS_EINVAL;
+  return int4_gemm_impl(x, ldx, packed, ld_packed, scale, ld_scale, scale_dtype, zero_point, ld_zero, tiles, y, ldy, M,
+                        N, K, group, workspace, workspace_bytes, stream);
 }
 
 int hs_int4_gemm_noalloc(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,
@@ -619,9 +640,9 @@ int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int
   return hsq::hip_code(hsq::launch_mid(hsq::W_INT4, a, p.BMI, p.NJ, p.NW, static_cast<hipStream_t>(stream)));
 }
 
-int hs_fp8_gemm(const void* x, int64_t ldx, const uint8_t* data, int64_t ld_data, const void* scale_inv,
-                int64_t ld_scale, int scale_dtype, void* y, int64_t ldy, int M, int N, int K, void* workspace,
-                int64_t workspace_bytes, void* stream) {
+static int fp8_gemm_impl(const void* x, int64_t ldx, const uint8_t* data, int64_t ld_data, const uint8_t* tiles,
+                         const void* scale_inv, int64_t ld_scale, int scale_dtype, void* y, int64_t ldy, int M, int N,
+                         int K, void* workspace, int64_t workspace_bytes, void* stream) {
   if (M < 0 || N < 0 || K < 0) return HS_EINVAL;
   if (M == 0 || N == 0) return HS_OK;
   if (K == 0) return HS_EUNSUPPORTED;
@@ -646,7 +667,23 @@ int hs_fp8_gemm(const void* x, int64_t ldx, const uint8_t* data, int64_t ld_data
   a.K = K;
   a.wvec = hsq::aligned16(data) && (ld_data % 16 == 0);
   a.tune = hsq::tuning().tune;
+  a.wtiles = tiles != nullptr && hsq::aligned16(tiles) && K % 128 == 0 && N % 16 == 0 ? tiles : nullptr;
   return hsq::run_gemm(hsq::W_FP8, a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int hs_fp8_gemm(const void* x, int64_t ldx, const uint8_t* data, int64_t ld_data, const void* scale_inv,
+                int64_t ld_scale, int scale_dtype, void* y, int64_t ldy, int M, int N, int K, void* workspace,
+                int64_t workspace_bytes, void* stream) {
+  return fp8_gemm_impl(x, ldx, data, ld_data, nullptr, scale_inv, ld_scale, scale_dtype, y, ldy, M, N, K, workspace,
+                       workspace_bytes, stream);
+}
+
+int hs_fp8_gemm_tiled(const void* x, int64_t ldx, const uint8_t* data, int64_t ld_data, const uint8_t* tiles,
+                      const void* scale_inv, int64_t ld_scale, int scale_dtype, void* y, int64_t ldy, int M, int N,
+                      int K, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (tiles == nullptr) return HS_EINVAL;
+  return fp8_gemm_impl(x, ldx, data, ld_data, tiles, scale_inv, ld_scale, scale_dtype, y, ldy, M, N, K, workspace,
+                       workspace_bytes, stream);
 }
 
 int hs_int4_dequant(const int32_t* packed, int64_t ld_packed, const void* scale, int64_t ld_scale, int scale_dtype,

@@ -84,6 +84,9 @@ def awq_linear(hidden, weight):
             flattened, weight.packed, weight.scale, weight.zero_point, n, k, weight.group_size
         )
         return out.reshape(shape)
+    tiles = getattr(weight, "tiles", None)  # load-time tiled copy (kernels/tiles.py)
+    if tiles is not None and not (tiles.is_cuda and tiles.device == hidden.device and tiles.is_contiguous()):
+        raise ValueError("INT4 weight tiles must be a contiguous tensor on the activation's GPU")
     with device_guard(hidden.device):
-        out = _native.int4_gemm(flattened, weight.packed, weight.scale, weight.zero_point, n, k, weight.group_size)
+        out = _native.int4_gemm(flattened, weight.packed, weight.scale, weight.zero_point, n, k, weight.group_size, tiles)
     return out.reshape(shape)

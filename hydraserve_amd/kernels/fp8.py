@@ -115,6 +115,9 @@ def fp8_linear(hidden, weight):
         # Dynamo/Inductor: the opaque custom op (hydraserve_amd/ops.py)
         out = torch.ops.hydraserve_amd.fp8_gemm(flattened, data, weight.scale_inv, output_features, input_features)
         return out.reshape(shape)
+    tiles = getattr(weight, "tiles", None)  # load-time tiled copy (kernels/tiles.py)
+    if tiles is not None and not (tiles.is_cuda and tiles.device == hidden.device and tiles.is_contiguous()):
+        raise ValueError("FP8 weight tiles must be a contiguous tensor on the activation's GPU")
     with device_guard(hidden.device):
-        out = _native.fp8_gemm(flattened, data, weight.scale_inv, output_features, input_features)
+        out = _native.fp8_gemm(flattened, data, weight.scale_inv, output_features, input_features, tiles)
     return out.reshape(shape)

@@ -141,6 +141,7 @@ def load_linear_weights(
     dtype: Any = None,
     host_fp8: Iterable[str] = (),
     fuse_gate_up: bool = False,
+    tile: bool = False,
 ) -> dict[str, Any]:
     """Every linear weight under ``prefix`` by base name.
 
@@ -148,8 +149,12 @@ def load_linear_weights(
     ``fuse_gate_up``: for each ``<p>.gate_proj.weight`` / ``<p>.up_proj.weight``
     pair, also ``<p>.gate_up_proj.weight`` (fused along N) and, for INT4,
     ``<p>.gate_up_proj.weight.interleaved`` (the fused SiLU kernel's layout).
+    ``tile``: device-resident INT4/FP8 weights (N % 16 == 0, K % 128 == 0) come
+    with the load-time tiled copy the block-major decode kernel reads
+    (kernels/tiles.py).
     """
     from ..kernels.mlp import interleave_gate_up
+    from ..kernels.tiles import tile_fp8_weight, tile_int4_weight
     from .linear import concatenate_linear_weights
 
     reader = CheckpointReader(model_dir)
@@ -168,4 +173,15 @@ def load_linear_weights(
             out[f"{stem}.gate_up_proj.weight"] = fused
             if isinstance(fused, PackedInt4Weight) and fused.original_shape[0] % 32 == 0:
                 out[f"{stem}.gate_up_proj.weight.interleaved"] = interleave_gate_up(fused)
+    if tile:
+        for name, w in list(out.items()):
+            if name.endswith(".interleaved"):
+                continue
+            n_k = getattr(w, "original_shape", None)
+            if n_k is None or n_k[0] % 16 or n_k[1] % 128:
+                continue
+            if isinstance(w, PackedInt4Weight) and w.group_size == 128:
+                out[name] = tile_int4_weight(w)
+            elif isinstance(w, BlockScaledFP8Weight) and w.data.device.type != "cpu":
+                out[name] = tile_fp8_weight(w)
     return out

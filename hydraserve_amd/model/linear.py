@@ -48,6 +48,16 @@ def _storage(weight) -> dict[str, int]:
     raise TypeError(f"unsupported fused linear weight: {type(weight)!r}")
 
 
+def _plain(weight):
+    """The reference dataclass of a weight (a load-time tiled copy is dropped:
+    its rows would no longer match after fusing or splitting)."""
+    if getattr(weight, "tiles", None) is None:
+        return weight
+    if isinstance(weight, PackedInt4Weight):
+        return PackedInt4Weight(weight.packed, weight.scale, weight.zero_point, weight.original_shape, weight.group_size)
+    return BlockScaledFP8Weight(weight.data, weight.scale_inv, weight.original_shape, weight.block_size)
+
+
 def _static(weight) -> tuple:
     """Everything besides the row count that fused parts must share."""
     if isinstance(weight, PackedInt4Weight):
@@ -71,6 +81,7 @@ def concatenate_linear_weights(parts):
 
     if not parts:
         return None
+    parts = [_plain(p) if isinstance(p, (PackedInt4Weight, BlockScaledFP8Weight)) else p for p in parts]
     kinds = {type(p) for p in parts}
     if len(kinds) != 1:
         return None
@@ -102,6 +113,7 @@ def split_linear_weight(fused, sizes: tuple[int, ...]):
 
     if isinstance(fused, torch.Tensor):
         return fused.split(sizes, dim=0)
+    fused = _plain(fused)
     fields = _storage(fused)
     views = []
     row = 0

@@ -123,6 +123,34 @@ int hs_fp8_gemm(const void* x, int64_t ldx,
                 void* workspace, int64_t workspace_bytes,
                 void* stream);
 
+/* hs_int4_gemm / hs_fp8_gemm with a load-time tiled copy of the weight
+ * (the "kernel-native layout" of the weight; same GPU branch of awq_linear /
+ * fp8_linear, hydraserve/kernels/awq.py:25-75, hydraserve/kernels/fp8.py:24-97).
+ * tiles: rows 16t..16t+15 of 128-wide K chunk c stored contiguously as tile
+ * (t, c) at byte (t * ceil(K/128) + c) * TB, TB = 1024 (INT4: 16 rows x 16
+ * int32 words) or 2048 (FP8: 16 rows x 128 bytes), each tile's rows in
+ * order: i.e. packed.view(N/16, 16, K/128, TB/16).permute(0, 2, 1, 3).
+ * Requires N % 16 == 0 and K % 128 == 0 for the tiles to be read; the
+ * row-major weight is still passed and used by the kernels that do not read
+ * tiles (the tiles serve the block-major decode kernel at 1..16 rows, where
+ * one load instruction then reads one contiguous tile).  Results are those of
+ * the untiled entry points to the same bars. */
+int hs_int4_gemm_tiled(const void* x, int64_t ldx,
+                       const int32_t* packed, int64_t ld_packed, const int32_t* tiles,
+                       const void* scale, int64_t ld_scale, int scale_dtype,
+                       const int32_t* zero_point, int64_t ld_zero,
+                       void* y, int64_t ldy,
+                       int M, int N, int K, int group,
+                       void* workspace, int64_t workspace_bytes,
+                       void* stream);
+int hs_fp8_gemm_tiled(const void* x, int64_t ldx,
+                      const uint8_t* data, int64_t ld_data, const uint8_t* tiles,
+                      const void* scale_inv, int64_t ld_scale, int scale_dtype,
+                      void* y, int64_t ldy,
+                      int M, int N, int K,
+                      void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
 /* out[N,K] = (q - z) * s rounded once to out_dtype (the dtype of the scale in
  * the reference).  GPU counterpart of dequantize_int4_weight
  * (hydraserve/kernels/awq.py:6-22); bit-exact. */

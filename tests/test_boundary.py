@@ -242,3 +242,34 @@ def test_noalloc_entry_point_validates_before_touching_the_device():
     assert L.hs_int4_gemm_noalloc(16, 256, 16, 32, 16, 2, 9, 16, 2, 16, 64, 1, 64, 256, 128, None) == 1
     assert L.hs_int4_gemm_noalloc(None, 0, None, 0, None, 0, 0, None, 0, None, 0, 0, 64, 256, 128, None) == 0
     assert b"scratch" in L.hs_error_string(4)
+
+
+def test_tiled_copies_round_trip_and_are_dropped_by_fuse_split():
+    from hydraserve_amd.kernels.tiles import TiledInt4Weight, tile_fp8_weight, tile_int4_weight, untile_int4
+
+    g = torch.Generator().manual_seed(3)
+    n, k = 48, 384
+    w = PackedInt4Weight(
+        torch.randint(-(2**31), 2**31 - 1, (n, k // 8), generator=g, dtype=torch.int32),
+        torch.rand(n, 3, generator=g).to(torch.bfloat16),
+        torch.randint(-(2**31), 2**31 - 1, (n // 8, 3), generator=g, dtype=torch.int32),
+        (n, k),
+    )
+    t = tile_int4_weight(w)
+    assert isinstance(t, TiledInt4Weight) and isinstance(t, PackedInt4Weight)
+    assert t.tiles.shape == (3, 3, 16, 16)
+    assert torch.equal(untile_int4(t.tiles, n, k), w.packed)
+    # tile (1, 2) = rows 16..31, words 32..47
+    assert torch.equal(t.tiles[1, 2], w.packed[16:32, 32:48])
+    f = BlockScaledFP8Weight(
+        torch.randint(0, 120, (32, 256), generator=g, dtype=torch.uint8).view(torch.float8_e4m3fn),
+        torch.ones(1, 2), (32, 256),
+    )
+    tf = tile_fp8_weight(f)
+    assert torch.equal(tf.tiles[1, 1], f.data.view(torch.uint8)[16:32, 128:256])
+    parts = hs.split_linear_weight(t, (16, 32))
+    assert all(type(p) is PackedInt4Weight for p in parts)
+    fused = hs.concatenate_linear_weights([t, t])
+    assert type(fused) is PackedInt4Weight and fused.original_shape == (96, k)
+    with pytest.raises(ValueError, match="N % 16"):
+        tile_int4_weight(PackedInt4Weight(w.packed[:8], w.scale[:8], w.zero_point[:1], (8, k)))

@@ -87,6 +87,18 @@ def test_reader_recognises_formats_and_reads_bit_exact(tmp_path, sharded):
         reader.tensor("nope")
 
 
+def test_load_with_tiles(tmp_path):
+    from hydraserve_amd.kernels.tiles import TiledFP8Weight, TiledInt4Weight, untile_int4
+
+    _write(tmp_path, sharded=False)
+    w = load_linear_weights(tmp_path, device="cpu", tile=True)
+    g = w[f"{P}.mlp.gate_proj.weight"]
+    assert isinstance(g, TiledInt4Weight)
+    assert torch.equal(untile_int4(g.tiles, 64, 256), g.packed)
+    assert isinstance(w[f"{P}.self_attn.o_proj.weight"], TiledFP8Weight)
+    assert not hasattr(w["lm_head.weight"], "tiles")
+
+
 def test_missing_checkpoint_is_an_error(tmp_path):
     with pytest.raises(FileNotFoundError):
         CheckpointReader(tmp_path)
