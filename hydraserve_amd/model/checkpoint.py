@@ -182,6 +182,6 @@ def load_linear_weights(
                 continue
             if isinstance(w, PackedInt4Weight) and w.group_size == 128:
                 out[name] = tile_int4_weight(w)
-            elif isinstance(w, BlockScaledFP8Weight) and w.data.device.type != "cpu":
+            elif isinstance(w, BlockScaledFP8Weight) and name not in host:  # streamed weights stay row-major
                 out[name] = tile_fp8_weight(w)
     return out
