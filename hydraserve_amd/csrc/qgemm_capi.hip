@@ -82,6 +82,7 @@ struct Tuning {
   int skinny_layout = -1;  // its (S, NB, KC) layout index (-1 = heuristic)
   int skinny_wg = 0;       // its workgroups per CU (0 = 1)
   int skinny_xd = -1;      // its largest M loading X fragments per wave (-1 = none)
+  int row_split_off = 0;   // 1: no two-pass row split at 129..256 rows on narrow outputs
 };
 
 int env_int(const char* name) {
@@ -121,6 +122,7 @@ const Tuning& tuning() {
     if (std::getenv("HS_SKINNY_LAYOUT") != nullptr) r.skinny_layout = env_int("HS_SKINNY_LAYOUT");
     r.skinny_wg = env_int("HS_SKINNY_WG");
     if (std::getenv("HS_SKINNY_XD") != nullptr) r.skinny_xd = env_int("HS_SKINNY_XD");
+    r.row_split_off = env_int("HS_ROW_SPLIT_OFF");
     return r;
   }();
   return t;
@@ -330,6 +332,24 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   if (!extents_ok(wt, a, a.N)) return HS_EUNSUPPORTED;
   a.xvec = aligned16(a.x) && (a.ldx % 8 == 0);
   const Tuning& tn = tuning();
+  // Narrow outputs (N < K) at 129..256 rows: too few 256x256 tiles to fill
+  // the chip (20 on a 5120-row output), so two passes of the 17..128-row
+  // streaming kernel over row halves measured faster (INT4 / FP8 down
+  // 17408->5120 at M=256: 102 / 100 us against 108 / 111 us; M=160: 80 vs
+  // 106 us).  Sequential on the stream, so they share the workspace.
+  if (!tn.row_split_off && a.M > 128 && a.M <= 256 && a.N < a.K && a.silu_mul == 0) {
+    GemmArgs lo = a, hi = a;
+    lo.M = 128;
+    hi.M = a.M - 128;
+    hi.x = a.x + 128 * a.ldx;
+    hi.y = a.y + 128 * a.ldy;
+    lo.xvec = hi.xvec = a.xvec && aligned16(hi.x);
+    if (lo.xvec && mid_ok(lo, wt)) {
+      const int rc = run_gemm(wt, lo, workspace, workspace_bytes, stream);
+      if (rc != HS_OK) return rc;
+      return run_gemm(wt, hi, workspace, workspace_bytes, stream);
+    }
+  }
   // Decode with at most 16 activation rows: row-partitioned kernels, one
   // partition per workgroup, no workspace.  Block-major when X fits in LDS.
   // The register-streamed kernel wins on narrow outputs (N < K) from 5
@@ -480,6 +500,12 @@ int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
                 hsq::make_plan(kind, M, N, K, kfull != 0, fast != 0, wide != 0, mid != 0, sk != 0).ws_bytes;
             best = b > best ? b : best;
           }
+  // the two row halves of the narrow-output split at 129..256 rows
+  if (M > 128 && M <= 256 && N < K) {
+    const int64_t lo = hs_gemm_workspace_bytes(kind, 128, N, K), hi = hs_gemm_workspace_bytes(kind, M - 128, N, K);
+    best = lo > best ? lo : best;
+    best = hi > best ? hi : best;
+  }
   return best;
 }
 

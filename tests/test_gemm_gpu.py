@@ -520,7 +520,8 @@ CONFIG4_SHAPES = [(10240, 5120), (5120, 8192), (12288, 5120)]  # qkv, o_proj, GD
     "m,n,k",
     [(8, 4096, 4096)]  # config 0
     + [(m, n, k) for m in (1, 4, 16, 64, 128, 512, 1024, 2048) for n, k in ((34816, 5120), (5120, 17408))]
-    + [(m, n, k) for m in (64, 1024) for n, k in CONFIG4_SHAPES],
+    + [(m, n, k) for m in (64, 1024) for n, k in CONFIG4_SHAPES]
+    + [(256, 5120, 17408), (160, 5120, 8192), (200, 5120, 17408)],  # narrow outputs split in two row passes
 )
 def test_int4_baseline_shapes_sampled_oracle(m, n, k):
     """Full-size configs 0, 1, 2 and 4 (gate_up and down also at M=1024, the
@@ -545,7 +546,7 @@ def test_int4_baseline_shapes_sampled_oracle(m, n, k):
     assert_gemm_close(y[:, cols], ref, what=f"m={m} {n}x{k}")
 
 
-@pytest.mark.parametrize("m", [1, 16, 64, 256, 2048])
+@pytest.mark.parametrize("m", [1, 16, 64, 200, 256, 2048])
 @pytest.mark.parametrize("n,k", [(34816, 5120), (5120, 17408)])
 def test_fp8_baseline_shapes_sampled_oracle(m, n, k):
     dev = _cuda()
