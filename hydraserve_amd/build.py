@@ -19,7 +19,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libhydraserve_amd.so"
 BUILD_DIR = PKG / "_build"
-SOURCES = ["qgemm_skinny.hip", "qgemm_decode.hip", "qgemm_stream.hip", "qgemm_rows.hip", "qgemm_gemv.hip", "qgemm_prefill.hip", "qgemm_wide.hip", "qgemm_mid.hip", "qgemm_dequant.hip", "hbm_probe.hip", "qgemm_capi.hip"]
+SOURCES = ["qgemm_tiled.hip", "qgemm_skinny.hip", "qgemm_decode.hip", "qgemm_stream.hip", "qgemm_rows.hip", "qgemm_gemv.hip", "qgemm_prefill.hip", "qgemm_wide.hip", "qgemm_mid.hip", "qgemm_dequant.hip", "hbm_probe.hip", "qgemm_capi.hip"]
 ARCH = os.environ.get("HS_OFFLOAD_ARCH", "gfx950")
 
 
@@ -73,7 +73,7 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as pool:
         objs = list(pool.map(compile_one, SOURCES))
     tmp = OUT.with_suffix(".so.tmp")
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")

@@ -35,6 +35,10 @@ bool gemv_ok(const GemmArgs& a, int wt, int P, int kw_pref, int* kw_out, int* ro
 hipError_t launch_gemv(int wt, const GemmArgs& a, int kw, hipStream_t stream);
 extern int gemv_rd;
 bool skinny_ok(const GemmArgs& a, int wt, int kc);
+bool tiled_ok(const GemmArgs& a, int wt);
+hipError_t launch_tiled(int wt, const GemmArgs& a, hipStream_t stream);
+int tm_slot_floats(int wt, int M);
+int tm_max_tpw(int wt, int M);
 hipError_t launch_skinny(int wt, const GemmArgs& a, int s, int nb, int kc, bool xd, hipStream_t stream);
 int skinny_slot_floats(int mt, int s, int nb);
 int skinny_bt(int s, int nb);
@@ -83,6 +87,10 @@ struct Tuning {
   int skinny_wg = 0;       // its workgroups per CU (0 = 1)
   int skinny_xd = -1;      // its largest M loading X fragments per wave (-1 = none)
   int row_split_off = 0;   // 1: no two-pass row split at 129..256 rows on narrow outputs
+  int tm_off = 0;          // 1: never use the tiled decode kernel
+  int tm_min_m = 0;        // smallest M for it (0 = default)
+  int tm_tpw = 0;          // its tiles per workgroup (0 = heuristic)
+  int tm_s = 0;            // its K ranges (0 = heuristic)
 };
 
 int env_int(const char* name) {
@@ -123,6 +131,10 @@ const Tuning& tuning() {
     r.skinny_wg = env_int("HS_SKINNY_WG");
     if (std::getenv("HS_SKINNY_XD") != nullptr) r.skinny_xd = env_int("HS_SKINNY_XD");
     r.row_split_off = env_int("HS_ROW_SPLIT_OFF");
+    r.tm_off = env_int("HS_TM_OFF");
+    r.tm_min_m = env_int("HS_TM_MIN_M");
+    r.tm_tpw = env_int("HS_TM_TPW");
+    r.tm_s = env_int("HS_TM_S");
     return r;
   }();
   return t;
@@ -162,6 +174,64 @@ struct Plan {
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 int stream_nb(int M) { return M <= 16 ? 8 : (M <= 32 ? 4 : 2); }
+
+// Tiled decode kernel: tile groups of `tpw` 16-row tiles over `splits` K
+// ranges of `cps` chunks, one workgroup each, at most one per CU.  The
+// estimate per chunk step is the larger of the CU's HBM bytes (its tiles plus
+// a share for the X chunk, an L2 hit) and the busiest wave's dequant + MFMA
+// work in byte equivalents; split groups add a settle.
+struct TmPlan {
+  int tpw = 0, splits = 0, cps = 0, P = 0;
+  int64_t ws_bytes = 0;
+};
+
+TmPlan tm_plan(int wt, int M, int N, int K) {
+  TmPlan best;
+  const int cus = device_cus();
+  const Tuning& tn = tuning();
+  const int64_t NT = N / 16, NC = K / 128;
+  const int mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  const double tb = wt == W_INT4 ? 1024.0 : 2048.0;
+  const double comp = wt == W_INT4 ? 2600.0 : 1000.0 + 250.0 * mb;
+  double best_est = 1e30;
+  const int cand[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
+  for (int s0 : cand) {
+    if (tn.tm_s > 0 && s0 != tn.tm_s) continue;
+    if (s0 > NC) break;
+    const int cps = static_cast<int>(cdiv(NC, s0));
+    const int S = static_cast<int>(cdiv(NC, cps));
+    int tpw = tn.tm_tpw > 0 ? tn.tm_tpw : static_cast<int>(cdiv(NT * S, cus));
+    if (tpw < 1) tpw = 1;
+    if (tpw > tm_max_tpw(wt, M)) continue;
+    const int64_t groups = cdiv(NT, tpw);
+    const int64_t P = groups * S;
+    if (P > 4 * cus || groups > kMaxTiles) continue;
+    const double waves_per_cu = P > cus ? static_cast<double>(cdiv(P, cus)) : 1.0;
+    const int tw = (tpw + 3) / 4;  // tiles per SIMD
+    const double mem = tpw * tb + 0.5 * mb * 4096.0;
+    const double cmp = tw * comp;
+    const double est = waves_per_cu * cps * (mem > cmp ? mem : cmp) + (S > 1 ? 40000.0 : 0.0);
+    if (est < best_est) {
+      best_est = est;
+      best.tpw = tpw;
+      best.splits = S;
+      best.cps = cps;
+      best.P = static_cast<int>(P);
+    }
+  }
+  if (best.P > 0)
+    best.ws_bytes = kCounterBytes + static_cast<int64_t>(best.P) * tm_slot_floats(wt, M) * 4;
+  return best;
+}
+
+// Measured on MI355X (gate_up 5120->34816, down 17408->5120, qkv): INT4 at
+// 1..4 rows stays on the row-major block-major / row-partitioned kernels
+// (gate_up M=4: 25.5 vs 27.9 us; down M=1: 17.2 vs 21.0 us); from 5 rows and
+// for FP8 at every row count the tiled kernel is faster.
+bool tm_min_ok(int wt, int M) {
+  const Tuning& tn = tuning();
+  return !tn.tm_off && M >= (tn.tm_min_m > 0 ? tn.tm_min_m : (wt == W_INT4 ? 5 : 1));
+}
 
 // Register-streamed decode kernel layouts: S 16-row blocks per wave, NB
 // block groups, KC K phases (NB * KC = 8 wavefronts).
@@ -332,6 +402,20 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   if (!extents_ok(wt, a, a.N)) return HS_EUNSUPPORTED;
   a.xvec = aligned16(a.x) && (a.ldx % 8 == 0);
   const Tuning& tn = tuning();
+  // Tiled weight copy: the tiled decode kernel (contiguous KiB weight loads);
+  // every other kernel reads the row-major weight.
+  if (a.wtiles != nullptr && tm_min_ok(wt, a.M) && tiled_ok(a, wt)) {
+    const TmPlan tp = tm_plan(wt, a.M, a.N, a.K);
+    if (tp.P > 0) {
+      if (tp.splits > 1 && (workspace == nullptr || workspace_bytes < tp.ws_bytes)) return HS_EWORKSPACE;
+      a.tpw = tp.tpw;
+      a.splits = tp.splits;
+      a.cps = tp.cps;
+      a.counters = reinterpret_cast<int*>(workspace);
+      a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + kCounterBytes);
+      return hip_code(launch_tiled(wt, a, stream));
+    }
+  }
   // Narrow outputs (N < K) at 129..256 rows: too few 256x256 tiles to fill
   // the chip (20 on a 5120-row output), so two passes of the 17..128-row
   // streaming kernel over row halves measured faster (INT4 / FP8 down
@@ -355,6 +439,7 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   // The register-streamed kernel wins on narrow outputs (N < K) from 5
   // (INT4) / 9 (FP8) activation rows; the row-partitioned kernels below keep
   // fewer rows and the wide outputs.
+  a.wtiles = nullptr;
   const bool skinny_auto = a.N < a.K && a.M >= (wt == W_INT4 ? 5 : 9);
   const bool use_skinny = tn.skinny != 2 && (tn.skinny == 1 || skinny_auto) && a.M <= 64 &&
                           skinny_ok(a, wt, skinny_layout(wt, a.M, a.K).kc);
@@ -367,8 +452,6 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   if (!use_skinny && !tn.gemv_off && a.M <= 16 && !gemv_narrow) {
     const int P = device_cus() * (tn.gemv_wg > 0 ? tn.gemv_wg : 1);
     int kw = 0, rows_max = 0;
-    // the tiled weight copy (if any) is read by this kernel only
-    if (a.wtiles != nullptr && !gemv_ok(a, wt, P, tn.gemv_kw > 0 ? tn.gemv_kw : 8, &kw, &rows_max)) a.wtiles = nullptr;
     if (gemv_ok(a, wt, P, tn.gemv_kw > 0 ? tn.gemv_kw : 8, &kw, &rows_max)) {
       a.P = P;
       a.T = a.K / 128;
@@ -376,7 +459,6 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
       return hip_code(launch_gemv(wt, a, kw, stream));
     }
   }
-  a.wtiles = nullptr;
   if (!use_skinny && !tn.rows_off && a.M <= (tn.rows_ms2_off ? 16 : 32)) {
     const int P = device_cus() * (tn.rows_wg > 0 ? tn.rows_wg : 1);
     int nblk = 0, ms = 1;
@@ -500,6 +582,11 @@ int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
                 hsq::make_plan(kind, M, N, K, kfull != 0, fast != 0, wide != 0, mid != 0, sk != 0).ws_bytes;
             best = b > best ? b : best;
           }
+  // the tiled decode kernel (calls that pass a tiled copy)
+  if (M <= 64 && N % 16 == 0 && K % 128 == 0) {
+    const int64_t b = hsq::tm_plan(kind, M, N, K).ws_bytes;
+    best = b > best ? b : best;
+  }
   // the two row halves of the narrow-output split at 129..256 rows
   if (M > 128 && M <= 256 && N < K) {
     const int64_t lo = hs_gemm_workspace_bytes(kind, 128, N, K), hi = hs_gemm_workspace_bytes(kind, M - 128, N, K);

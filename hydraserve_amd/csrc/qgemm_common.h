@@ -56,9 +56,11 @@ struct GemmArgs {
   int tune;           // kernel-specific experiment bits (0 = defaults)
   int silu_mul;       // 1: W rows interleave gate and up in 16-row blocks and
                       // y [M, N/2] receives silu(gate) * up
-  const void* wtiles;  // optional load-time copy of W in 16-row tiles: tile
-                       // (n/16, k/128) holds rows 16t..16t+15 of that 128-wide
-                       // K chunk contiguously (1 KiB INT4, 2 KiB FP8); null: none
+  const void* wtiles;  // optional load-time copy of W in 16-row tiles (read by
+                       // the tiled decode kernel only; layout in qgemm_tiled.hip)
+  int tpw;            // tiled decode kernel: 16-row tiles per workgroup
+  int splits;         // tiled decode kernel: K ranges per tile group
+  int cps;            // tiled decode kernel: 128-wide K chunks per K range
 };
 
 // Row partitions of the row-partitioned decode kernels: rows [*r0, *r1) of
@@ -66,12 +68,7 @@ struct GemmArgs {
 // SiLU-and-mul epilogue (a.silu_mul, N a multiple of 32) an even split of the
 // N/32 gate/up block pairs, so both blocks of a pair land in one workgroup.
 __host__ __device__ inline void row_partition(const GemmArgs& a, int p, int* r0, int* r1) {
-  if (a.wtiles != nullptr && !a.silu_mul) {
-    // tiled weights: whole 16-row tiles per workgroup
-    const int64_t nt = a.N / 16;
-    *r0 = 16 * static_cast<int>(p * nt / a.P);
-    *r1 = 16 * static_cast<int>((p + 1) * nt / a.P);
-  } else if (a.silu_mul) {
+  if (a.silu_mul) {
     const int64_t np = a.N / 32;
     *r0 = 32 * static_cast<int>(p * np / a.P);
     *r1 = 32 * static_cast<int>((p + 1) * np / a.P);
@@ -83,7 +80,6 @@ __host__ __device__ inline void row_partition(const GemmArgs& a, int p, int* r0,
 
 // The largest partition row_partition gives with P workgroups.
 __host__ __device__ inline int row_partition_max(const GemmArgs& a, int P) {
-  if (a.wtiles != nullptr && !a.silu_mul) return 16 * static_cast<int>((a.N / 16 + P - 1) / P);
   return a.silu_mul ? 32 * static_cast<int>((a.N / 32 + P - 1) / P) : (a.N + P - 1) / P;
 }
 

@@ -107,15 +107,8 @@ __global__ __launch_bounds__(64 * KW) void qgemm_gemv_kernel(GemmArgs a) {
   const int z0 = r0 >> 3, zn = ((r1 - 1) >> 3) - z0 + 1;
   const int b0 = r0 >> 7, bn = ((r1 - 1) >> 7) - b0 + 1;
 
-  // Row-major W, or (a.wtiles) the load-time tiled copy: tile (n/16, c) of
-  // TB bytes holds the 16 rows' chunk c contiguously, so one load
-  // instruction reads one contiguous KiB.
-  const bool tiled = a.wtiles != nullptr;
-  constexpr int TB = WT == W_INT4 ? 1024 : 2048;
-  const __amdgpu_buffer_rsrc_t rw =
-      tiled ? make_rsrc(a.wtiles, static_cast<int64_t>(a.N / 16) * GC * TB)
-            : make_rsrc(a.w, static_cast<int64_t>(a.N - 1) * (WT == W_INT4 ? a.ldw * 4 : a.ldw) +
-                                 (WT == W_INT4 ? a.K / 2 : a.K));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(
+      a.w, static_cast<int64_t>(a.N - 1) * (WT == W_INT4 ? a.ldw * 4 : a.ldw) + (WT == W_INT4 ? a.K / 2 : a.K));
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (static_cast<int64_t>(M - 1) * a.ldx + a.K) * 2);
   const int rb = static_cast<int>(WT == W_INT4 ? a.ldw * 4 : a.ldw);  // bytes per weight row
 
@@ -127,14 +120,11 @@ __global__ __launch_bounds__(64 * KW) void qgemm_gemv_kernel(GemmArgs a) {
   // Load cursor (runs RD steps ahead, stops at the last step).
   int lb = 0, li = 0, lstep = 0;
   auto row_off = [&](int b) __attribute__((always_inline)) {
-    if (tiled)  // r0 is a multiple of 16; lane (l16, h) at row l16's byte CB/4*h of the tile
-      return static_cast<uint32_t>(((r0 >> 4) + b) * GC * TB) + static_cast<uint32_t>(l16 * D::CB) +
-             (WT == W_INT4 ? 16u : 32u) * h;
     int row = r0 + 16 * b + l16;
     row = row < r1 ? row : r1 - 1;
     return static_cast<uint32_t>(row * rb) + (WT == W_INT4 ? 16u : 32u) * h;
   };
-  const int cstride = tiled ? TB : D::CB;
+  const int cstride = D::CB;
   uint32_t lwoff = row_off(0);
   auto load_step = [&](typename D::Slot& s) __attribute__((always_inline)) {
     const uint32_t so = static_cast<uint32_t>((cs + li) * cstride);
@@ -403,7 +393,6 @@ bool gemv_ok(const GemmArgs& a, int wt, int P, int kw_pref, int* kw_out, int* ro
   // Only with kw_pref wavefronts: fewer leave too few loads in flight (a
   // layout that does not fit goes to the row-partitioned kernel instead).
   if (a.silu_mul && (wt != W_INT4 || a.N % 32 != 0)) return false;
-  if (a.wtiles != nullptr && (a.N % 16 != 0 || (static_cast<int64_t>(a.N / 16) * (a.K / 128) * (wt == W_INT4 ? 1024 : 2048)) >= (int64_t{1} << 31))) return false;
   const int nr_max = row_partition_max(a, P);
   const int kw = kw_pref;
   if (a.K / 128 < kw) return false;  // every wavefront gets at least one chunk

@@ -1,0 +1,526 @@
+// Decode-regime (1..64 activation rows) quantized weight GEMM over the
+// load-time tiled weight copy, for gfx950.
+//
+// INT4 tile words keep their K range (word j of a row's chunk: K 8j .. 8j+7)
+// with the nibbles paired for the MFMA operand: nibble i (i < 4) holds
+// K 8j + 2i and nibble i + 4 holds K 8j + 2i + 1, so ((w >> 4i) & 0x000F000F)
+// puts two consecutive-K weights in the two halves of a dword
+// (hydraserve_amd/kernels/tiles.py makes the copy).
+//
+// Replaces the Triton launches of hydraserve/kernels/awq.py:52-74
+// (_awq_gemm_kernel, awq.py:82-142) and hydraserve/kernels/fp8.py:68-96
+// (_fp8_gemm_kernel, fp8.py:104-168) when the weight carries a tiled copy:
+// tile (t, c) = rows 16t..16t+15 of the 128-wide K chunk c, stored
+// contiguously (INT4: 16 rows x 64 bytes = 1 KiB; FP8: 16 rows x 128 bytes =
+// 2 KiB) at byte (t * K/128 + c) * tile_bytes.  Every weight load instruction
+// therefore reads one contiguous KiB, the access HBM serves best, where the
+// row-major checkpoint layout gives 16-32 pieces of 32-64 bytes on distinct
+// DRAM pages.
+//
+// Work split.  The N/16 tiles are cut into groups of `tpw` consecutive tiles
+// and K into `splits` ranges of `cps` chunks; workgroup p takes tile group
+// p / splits over K range p % splits.  Its four wavefronts own the group's
+// tiles round-robin (wave w: local tiles w, w+4, w+8) and walk the K range
+// together, one chunk per step:
+//   * the chunk's X tile [16*MB rows x 128] (shared by the four waves), each
+//     wave's weight tiles, and their scales / zero-point words go global ->
+//     LDS by LDS-DMA into a ring of D chunk slots, D-1 chunks ahead;
+//   * per step every wave waits for its own loads of the chunk, one barrier
+//     makes the other waves' X loads visible, and the slot of the previous
+//     chunk (which every wave has finished reading) takes the next loads;
+//   * weights are dequantised in registers to the reference's values,
+//     INT4 bf16_rne((q - z) * s) (awq.py:18-22, 136-137) via v_fma_mix on the
+//     fp16 1024+q, FP8 e4m3 -> bf16 exactly with the block scale applied to
+//     the chunk's fp32 MFMA result, and feed v_mfma_f32_16x16x32_bf16:
+//     lane (n, p) = (lane % 16, lane / 16) supplies weight row n and X row n of
+//     each 16-row block, K offsets 32p + 8s .. +8 at step s.
+// With one K range the workgroup stores bf16 Y directly.  With several, each
+// workgroup writes an fp32 partial of its tile group, and the last of the
+// group's workgroups to arrive sums the partials in K-range order
+// (deterministic) and stores Y.
+//
+// LDS slot layout (bytes): X rows r = 0 .. 16*MB-1 at 256r, the 16-byte
+// K segment g at ((g ^ (r & 15)) * 16); per wave its TW weight tiles (INT4:
+// 16-byte part p of row n at 64n + 16((p + n/4) & 3); FP8: part q of row n at
+// 128n + 16((q + n/2) & 7)), so the reads of 8 consecutive lanes hit distinct
+// banks; per wave 64 scale dwords and (INT4) 64 zero-point dwords, lane
+// 16i + n holding tile i's row n.
+#include <cstdlib>
+#include <type_traits>
+
+#include "qgemm_ops.h"
+
+namespace hsq {
+
+constexpr int kTmLds = 160 * 1024;
+
+struct TmRsrc {
+  __amdgpu_buffer_rsrc_t x, w, s, z;
+};
+
+template <int WT, int MB, int TW, int NW>
+struct Tm {
+  static constexpr int TB = WT == W_INT4 ? 1024 : 2048;  // bytes of one tile
+  static constexpr int LPT = TB / 1024;                  // 16-byte loads per lane per tile
+  static constexpr int XB = MB * 4096;                   // X bytes of a chunk
+  static constexpr int XI = XB / 1024;                   // 1 KiB X loads per chunk
+  // D: chunks of the weight / scale ring (D-1 in flight; the weights of a
+  // slot live in registers, TW * LPT * 4 VGPRs).  R: chunks per X round
+  // (D a multiple of R); X rounds are double-buffered in LDS and the
+  // workgroup meets at one barrier per round.
+  static constexpr int D = WT == W_INT4 ? 8 : (MB == 1 ? 6 : 4);
+  static constexpr int R = WT == W_INT4 ? (MB <= 2 ? 4 : 2) : (MB == 1 ? 3 : 2);
+  // R < D: the X of round 0 is issued inside the prologue, whose loads then
+  // come in the same order as in every later round.
+  static_assert(D % R == 0 && R < D, "X rounds tile the ring");
+  static constexpr int XR = R * XB;                      // X bytes of a round
+  static constexpr int LXR = (R * XI + NW - 1) / NW;     // X loads per wave per round
+  static constexpr int SB = NW * 256;
+  static constexpr int ZB = WT == W_INT4 ? NW * 256 : 0;
+  static constexpr int SLOTB = SB + ZB;
+  static_assert(2 * XR + D * SLOTB + 1024 + 256 <= kTmLds, "LDS");
+  static constexpr int SLOT = NW * TW * MB * 256;  // floats of one workgroup's partial
+
+  struct Smem {
+    __attribute__((aligned(1024))) uint8_t xs[2][XR];
+    __attribute__((aligned(1024))) uint8_t ring[D][SLOTB];
+    uint8_t junk[1024];  // target of the X loads that carry no data
+    int flag;
+  };
+
+  // Buffer accesses (kept out of the kernel's lambdas).
+  static __device__ __forceinline__ void dma(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int bytes, uint32_t voff,
+                                             uint32_t soff) {
+    if (bytes == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
+    else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 4, voff, soff, 0, 0);
+  }
+  static __device__ __forceinline__ u32x4_t wload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  }
+};
+
+// Round starts (steps t = 0 mod R) among steps lo .. hi (may be negative).
+constexpr int tm_round_starts(int lo, int hi, int R) {
+  int n = 0;
+  for (int t = lo; t <= hi; ++t) n += (((t % R) + R) % R) == 0;
+  return n;
+}
+
+template <int WT, int SDT, int MB, int TW, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
+  using C = Tm<WT, MB, TW, NW>;
+  constexpr int D = C::D;
+  constexpr int LPT = C::LPT;
+  __shared__ typename C::Smem sm;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, n = lane & 15, p4 = lane >> 4;
+  const int NC = a.K >> 7;
+  const int NT = a.N >> 4;
+  const int g = blockIdx.x / a.splits, sp = blockIdx.x - g * a.splits;
+  const int t0 = g * a.tpw;
+  const int nt = (NT - t0) < a.tpw ? (NT - t0) : a.tpw;       // tiles of the group
+  const int ntw = nt > wave ? (nt - wave + NW - 1) / NW : 0;  // of this wave (uniform)
+  const int c0 = sp * a.cps;
+  const int nk = (NC - c0) < a.cps ? (NC - c0) : a.cps;
+  if (nt <= 0 || nk <= 0) return;
+
+  TmRsrc rs;
+  rs.x = make_rsrc(a.x, (static_cast<int64_t>(a.M - 1) * a.ldx + a.K) * 2);
+  rs.w = make_rsrc(a.wtiles, static_cast<int64_t>(NT) * NC * C::TB);
+  // FP8 instances read the scale dtype at run time.
+  const int ses = WT == W_INT4 ? (SDT == SCALE_F32 ? 4 : 2) : (a.sdt == SCALE_F32 ? 4 : 2);
+  const int64_t s_rows = WT == W_INT4 ? a.N : (a.N + 127) / 128;
+  rs.s = make_rsrc(a.scale, (((s_rows - 1) * a.lds + ((a.K + 127) >> 7)) * ses + 3) & ~int64_t(3));
+  rs.z = WT == W_INT4 ? make_rsrc(a.zero, ((static_cast<int64_t>(a.N + 7) >> 3) * a.ldz) * 4) : rs.w;
+
+  // X load q of a round is the round's 1 KiB X load idx = wave + NW*q:
+  // chunk idx / XI of the round, LDS bytes (idx % XI)*1024 + 16*lane of that
+  // chunk's X, i.e. row r, K segment ((byte >> 4) & 15) ^ (r & 15).  Lanes of
+  // rows at or past M read out of the buffer's range (no memory access; their
+  // LDS bytes only reach output rows that are never stored).  Loads past the
+  // round's X go to the junk area, entirely out of range, so every wave
+  // issues LXR loads per round with no branches, which keeps the compiler's
+  // count of loads in flight exact.
+  constexpr uint32_t kOut = 0x80000000u;
+  uint32_t xo[C::LXR];
+  uint32_t xl[C::LXR];  // LDS byte offset of the load inside the X round (or ~0: junk)
+#pragma unroll
+  for (int q = 0; q < C::LXR; ++q) {
+    const int idx = wave + NW * q;
+    const int cr = idx / C::XI, blk = idx - cr * C::XI;
+    const int b = 1024 * blk + 16 * lane;
+    const int r = b >> 8;
+    const int seg = ((b >> 4) & 15) ^ (r & 15);
+    const bool on = idx < C::R * C::XI && r < a.M;
+    xo[q] = on ? static_cast<uint32_t>(r * static_cast<uint32_t>(a.ldx) * 2u + cr * 256 + seg * 16) : kOut;
+    xl[q] = idx < C::R * C::XI ? static_cast<uint32_t>(cr * C::XB + 1024 * blk) : 0xFFFFFFFFu;
+  }
+  // The wave's tiles; missing ones repeat tile t0 (loaded, never used).
+  int tt[TW];
+#pragma unroll
+  for (int i = 0; i < TW; ++i) {
+    const int j = wave + NW * i;
+    tt[i] = t0 + (j < nt ? j : 0);
+  }
+  // Weight byte offset of the lane's 16-byte load h of tile i at chunk 0.
+  // INT4: row n, bytes 16p .. +16 (K 32p + 8s + e at step s).  FP8: row n,
+  // bytes 64h + 16p .. +16 (K 64(s/2) + 16p + 8(s%2) + e at step s).
+  uint32_t wo[TW][LPT];
+#pragma unroll
+  for (int i = 0; i < TW; ++i)
+#pragma unroll
+    for (int h = 0; h < LPT; ++h) {
+      const uint32_t inner =
+          WT == W_INT4 ? static_cast<uint32_t>(64 * n + 16 * p4) : static_cast<uint32_t>(128 * n + 64 * h + 16 * p4);
+      wo[i][h] = static_cast<uint32_t>(tt[i]) * static_cast<uint32_t>(NC) * C::TB + inner;
+    }
+  // Scale / zero-point source of lane 16i + n (tile i of the wave, row n) at chunk 0.
+  const int li = (lane >> 4) < TW ? (lane >> 4) : TW - 1;
+  int64_t se0;
+  if constexpr (WT == W_INT4) se0 = static_cast<int64_t>(16 * tt[li] + n) * a.lds;
+  else se0 = static_cast<int64_t>((16 * tt[li]) >> 7) * a.lds;
+  const uint32_t zo0 = WT == W_INT4 ? static_cast<uint32_t>(((16 * tt[li] + n) >> 3) * a.ldz) * 4u : 0u;
+
+  // INT4 group rewrite (128 + q as bf16, one v_and_or_b32 per two weights)
+  // where the per-element correction stays cheaper than exact dequantisation.
+  constexpr bool REW = WT == W_INT4 && MB <= 2;
+  const uint32_t nib_mask = opaque_and(0x000F000Fu, 0xFFFFFFFFu);
+  const uint32_t magic = opaque_and(0x64006400u, 0xFFFFFFFFu);
+  const uint32_t magic_bf = opaque_and(0x43004300u, 0xFFFFFFFFu);
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+
+  f32x4_t acc[TW][MB];
+#pragma unroll
+  for (int i = 0; i < TW; ++i)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[i][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // The chunk loop for a wave with NTW real tiles (NTW uniform per wave):
+  // no dummy tiles are loaded or computed, and the loop body has no branches,
+  // so the compiler's own load-wait tracking stays exact across iterations.
+  // A wave's vmcnt counts only its own loads, so waves with different NTW
+  // (different loads per chunk) still meet at the same barriers.
+  auto run = [&](auto ntc) __attribute__((always_inline)) {
+    constexpr int NTW = decltype(ntc)::value;
+    constexpr int R = C::R;
+    // loads per wave per chunk: scales, (INT4) zero points, weights
+    constexpr int Lc = (NTW > 0 ? 1 + (WT == W_INT4 ? 1 : 0) : 0) + NTW * LPT;
+    u32x4_t W[D][NTW > 0 ? NTW : 1][LPT];  // weight ring (registers)
+
+    // X of round rho (chunks rho*R ..) into X buffer rho % 2; rounds past the
+    // range read harmless in-range or out-of-range bytes that nothing uses.
+    auto issue_x = [&](int rho) __attribute__((always_inline)) {
+      uint8_t* base = &sm.xs[rho & 1][0];
+      const int cf = c0 + (rho < 0 ? 0 : rho) * R;
+      const uint32_t kx = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(cf) * 256u);
+#pragma unroll
+      for (int q = 0; q < C::LXR; ++q)
+        C::dma(rs.x, (rho < 0 || xl[q] == 0xFFFFFFFFu) ? sm.junk : base + xl[q], 16, rho < 0 ? kOut : xo[q], kx);
+    };
+    // Scales, zero points and weights of chunk k (clamped) into ring slot J.
+    // (J is a constant once the loops below are unrolled, so W[J] stays in
+    // registers.)
+    auto issue = [&](int J, int k) __attribute__((always_inline)) {
+      if constexpr (NTW > 0) {
+        k = k < nk ? k : nk - 1;
+        const int c = c0 + k;
+        uint8_t* base = &sm.ring[J][0];
+        const uint32_t sb = static_cast<uint32_t>((se0 + c) * ses) & ~3u;
+        C::dma(rs.s, base + wave * 256, 4, sb, 0);
+        if constexpr (WT == W_INT4)
+          C::dma(rs.z, base + C::SB + wave * 256, 4, zo0 + static_cast<uint32_t>(c) * 4u, 0);
+        const uint32_t kw = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c) * C::TB);
+#pragma unroll
+        for (int i = 0; i < NTW; ++i)
+#pragma unroll
+          for (int h = 0; h < LPT; ++h) W[J][i][h] = C::wload(rs.w, wo[i][h], kw);
+      }
+    };
+
+    // Chunk k from ring slot J.
+    auto compute = [&](int J, int k) __attribute__((always_inline)) {
+      if constexpr (NTW > 0) {
+        const uint8_t* xchunk = &sm.xs[(k / R) & 1][0] + (J % R) * C::XB;
+        const int c = c0 + k;
+        const uint8_t* sbase = &sm.ring[J][0] + wave * 256;
+        uint32_t sd[NTW], zd[NTW];
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+          sd[i] = *reinterpret_cast<const uint32_t*>(sbase + (WT == W_INT4 ? (16 * i + n) * 4 : (16 * i) * 4));
+          zd[i] = WT == W_INT4 ? *reinterpret_cast<const uint32_t*>(sbase + C::SB + (16 * i + n) * 4) : 0u;
+        }
+        bf16x8_t A[MB][4];
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+          for (int st = 0; st < 4; ++st) {
+            const int gseg = WT == W_INT4 ? 4 * p4 + st : 8 * (st >> 1) + 2 * p4 + (st & 1);
+            A[b][st] = __builtin_bit_cast(
+                bf16x8_t, *reinterpret_cast<const u32x4_t*>(xchunk + (16 * b + n) * 256 + ((gseg ^ n) * 16)));
+          }
+        // Group rewrite: the per-row sums of X over the chunk, Xg, from an
+        // all-ones MFMA (same layout as the results).
+        f32x4_t xg[MB];
+        if constexpr (REW) {
+#pragma unroll
+          for (int b = 0; b < MB; ++b) {
+            xg[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+              xg[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[b][st], ones, xg[b], 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+          const int t = tt[i];
+          if constexpr (WT == W_INT4) {
+            const int64_t e = static_cast<int64_t>(16 * t + n) * a.lds + c;
+            float s;
+            if constexpr (SDT == SCALE_F32) s = __uint_as_float(sd[i]);
+            else if constexpr (SDT == SCALE_BF16) s = __uint_as_float((sd[i] >> ((e & 1) * 16)) << 16);
+            else s = __half2float(__ushort_as_half(static_cast<unsigned short>(sd[i] >> ((e & 1) * 16))));
+            const uint32_t z = (zd[i] >> ((n & 7) * 4)) & 0xFu;
+            if constexpr (REW) {
+              // acc += s * (sum x (128+q) - (128+z) * Xg)
+              f32x4_t T[MB];
+#pragma unroll
+              for (int b = 0; b < MB; ++b) T[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int st = 0; st < 4; ++st) {
+                const bf16x8_t B = int4_operand(W[J][i][0][st], nib_mask, magic_bf);
+#pragma unroll
+                for (int b = 0; b < MB; ++b)
+                  T[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[b][st], B, T[b], 0, 0, 0);
+              }
+              const float zc = static_cast<float>(128u + z);
+#pragma unroll
+              for (int b = 0; b < MB; ++b)
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2)
+                  acc[i][b][e2] = __builtin_fmaf(s, __builtin_fmaf(-zc, xg[b][e2], T[b][e2]), acc[i][b][e2]);
+            } else {
+              // exact: bf16_rne((q - z) * s), fp16 1024+q through v_fma_mix
+              const float zp = static_cast<float>(1024u + z);
+              const float cc = SDT == SCALE_F32 ? zp : -(zp * s);
+#pragma unroll
+              for (int st = 0; st < 4; ++st) {
+                typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+                const uint32_t w = W[J][i][0][st];
+                float f[8];
+#pragma unroll
+                for (int sh = 0; sh < 4; ++sh) {
+                  const f16x2_t v = __builtin_bit_cast(f16x2_t, insert_nibbles(nib_mask, w >> (4 * sh), magic));
+                  if constexpr (SDT == SCALE_F32) {
+                    f[2 * sh] = (static_cast<float>(v[0]) - cc) * s;
+                    f[2 * sh + 1] = (static_cast<float>(v[1]) - cc) * s;
+                  } else {
+                    f[2 * sh] = __builtin_fmaf(static_cast<float>(v[0]), s, cc);
+                    f[2 * sh + 1] = __builtin_fmaf(static_cast<float>(v[1]), s, cc);
+                  }
+                }
+                u32x4_t pb;
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) pb[e2] = pack_bf16x2(f[2 * e2], f[2 * e2 + 1]);
+                const bf16x8_t B = __builtin_bit_cast(bf16x8_t, pb);
+#pragma unroll
+                for (int b = 0; b < MB; ++b)
+                  acc[i][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[b][st], B, acc[i][b], 0, 0, 0);
+              }
+            }
+          } else {
+            const int64_t e = static_cast<int64_t>((16 * t) >> 7) * a.lds + c;
+            float s;
+            if (a.sdt == SCALE_F32) s = __uint_as_float(sd[i]);
+            else if (a.sdt == SCALE_BF16) s = __uint_as_float((sd[i] >> ((e & 1) * 16)) << 16);
+            else s = __half2float(__ushort_as_half(static_cast<unsigned short>(sd[i] >> ((e & 1) * 16))));
+            f32x4_t T[MB];
+#pragma unroll
+            for (int b = 0; b < MB; ++b) T[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+              const u32x4_t& q = W[J][i][st >> 1];
+              const bf16x8_t B = fp8_operand(q[2 * (st & 1)], q[2 * (st & 1) + 1]);
+#pragma unroll
+              for (int b = 0; b < MB; ++b)
+                T[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[b][st], B, T[b], 0, 0, 0);
+            }
+#pragma unroll
+            for (int b = 0; b < MB; ++b)
+#pragma unroll
+              for (int e2 = 0; e2 < 4; ++e2) acc[i][b][e2] = __builtin_fmaf(T[b][e2], s, acc[i][b][e2]);
+          }
+        }
+      }
+    };
+
+    // Step J of the unrolled ring (chunk k = k0 + J, k0 a multiple of D).
+    // Loads are issued in a fixed order: at a round start (J % R == 0) the X
+    // of the next round, then at every step the chunk D-1 ahead.  The wait
+    // before the step leaves in flight exactly the loads issued after the ones
+    // it needs: chunk k's group, and at a round start also this round's X.
+    auto step = [&](auto jc, int k) __attribute__((always_inline)) {
+      constexpr int J = decltype(jc)::value;
+      constexpr int after_g = (D - 2) * Lc + C::LXR * tm_round_starts(J - D + 2, J - 1, R);
+      constexpr int after_x = R * Lc;
+      constexpr int later = (J % R == 0 && after_x < after_g) ? after_x : after_g;
+      static_assert(later <= 63, "vmcnt range");
+      __builtin_amdgcn_s_waitcnt((later & 15) | ((later >> 4) << 14) | 0x0F70);
+      if constexpr (J % R == 0) {
+        // This round's X (every wave's share) has landed, and every wave is
+        // done with the previous round, whose buffer takes the next round.
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue_x(k / R + 1);
+      }
+      issue((J + D - 1) % D, k + D - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(J, k);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Prologue: the loads of steps -(D-1) .. -1 in steady-state order (X
+    // rounds before round 0 carry no data).
+#pragma unroll
+    for (int t = -(D - 1); t < 0; ++t) {
+      if (((t % R) + R) % R == 0) issue_x(t / R + 1);
+      issue(t + D - 1, t + D - 1);
+    }
+    int k0 = 0;
+    // Whole rounds of the ring: no branch inside the loop body.
+    for (; k0 + D <= nk; k0 += D) {
+#define HS_TM_STEP(J) if constexpr ((J) < D) step(std::integral_constant<int, (J)>{}, k0 + (J));
+      HS_TM_STEP(0) HS_TM_STEP(1) HS_TM_STEP(2) HS_TM_STEP(3) HS_TM_STEP(4) HS_TM_STEP(5) HS_TM_STEP(6) HS_TM_STEP(7)
+    }
+    // The remaining chunks (fewer than D), after the loop.
+#define HS_TM_REST(J) if constexpr ((J) < D - 1) { if (k0 + (J) < nk) step(std::integral_constant<int, (J)>{}, k0 + (J)); }
+    HS_TM_REST(0) HS_TM_REST(1) HS_TM_REST(2) HS_TM_REST(3) HS_TM_REST(4) HS_TM_REST(5) HS_TM_REST(6)
+#undef HS_TM_STEP
+#undef HS_TM_REST
+  };
+  if (ntw >= TW) run(std::integral_constant<int, TW>{});
+  else if (TW >= 3 && ntw == 2) run(std::integral_constant<int, (TW >= 3 ? 2 : 0)>{});
+  else if (ntw == 1) run(std::integral_constant<int, 1>{});
+  else run(std::integral_constant<int, 0>{});
+  // Drain the clamped prefetches before any exit.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+
+  // Lane (n, p4), register e of block (i, b): row 16b + 4p4 + e, column 16 tt[i] + n.
+  if (a.splits == 1) {
+#pragma unroll
+    for (int i = 0; i < TW; ++i) {
+      if (i >= ntw) continue;
+      const int col = 16 * tt[i] + n;
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int m = 16 * b + 4 * p4 + e2;
+          if (m < a.M) a.y[static_cast<int64_t>(m) * a.ldy + col] = to_bf16_bits(acc[i][b][e2]);
+        }
+    }
+    return;
+  }
+  const auto pr = partial_rsrc(a.partials);
+  auto poff = [&](int pp, int i, int b) __attribute__((always_inline)) {
+    return static_cast<uint32_t>((static_cast<int64_t>(pp) * C::SLOT / 4 + ((wave * TW + i) * MB + b) * 64 + lane) *
+                                 16);
+  };
+#pragma unroll
+  for (int i = 0; i < TW; ++i)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) store_partial4(pr, poff(blockIdx.x, i, b), acc[i][b]);
+  if (!arrive_last(a.counters, g, a.splits, &sm.flag)) return;
+  f32x4_t sum[TW][MB];
+#pragma unroll
+  for (int i = 0; i < TW; ++i)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) sum[i][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < a.splits; ++q) {
+    const int pp = g * a.splits + q;
+    f32x4_t v[TW][MB];
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) v[i][b] = load_partial4(pr, poff(pp, i, b));
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) sum[i][b] += v[i][b];
+  }
+#pragma unroll
+  for (int i = 0; i < TW; ++i) {
+    if (i >= ntw) continue;
+    const int col = 16 * tt[i] + n;
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const int m = 16 * b + 4 * p4 + e2;
+        if (m < a.M) a.y[static_cast<int64_t>(m) * a.ldy + col] = to_bf16_bits(sum[i][b][e2]);
+      }
+  }
+  reset_counter(a.counters, g);
+}
+
+// Layout: eight waves (two per SIMD, so one wave's dequantisation overlaps
+// the other's MFMAs and LDS latencies) of up to 2 tiles; FP8 above 32 rows
+// keeps four waves of up to 3 tiles (eight would spill registers).
+// Experiment switch: HS_TM_NW4=1 keeps four waves of up to 3 tiles above 32 rows.
+bool tm_nw4() {
+  static const bool v = [] {
+    const char* e = std::getenv("HS_TM_NW4");
+    return e != nullptr && e[0] == '1';
+  }();
+  return v;
+}
+
+int tm_mb(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
+int tm_nw(int wt, int M) { return M <= 32 || (wt == W_INT4 && !tm_nw4()) ? 8 : 4; }
+int tm_tw(int wt, int M) { return tm_nw(wt, M) == 8 ? 2 : 3; }
+int tm_max_tpw(int wt, int M) { return tm_nw(wt, M) * tm_tw(wt, M); }
+int tm_slot_floats(int wt, int M) { return tm_nw(wt, M) * tm_tw(wt, M) * tm_mb(M) * 256; }
+
+// Tiled copy present, M <= 64, N a multiple of 16, K a multiple of 128, every
+// buffer range below 2^31 bytes.
+bool tiled_ok(const GemmArgs& a, int wt) {
+  if (a.wtiles == nullptr || a.M <= 0 || a.M > 64 || a.N % 16 != 0 || a.K % 128 != 0 || a.silu_mul || !a.xvec)
+    return false;
+  if ((reinterpret_cast<uintptr_t>(a.scale) & 3) != 0 || (reinterpret_cast<uintptr_t>(a.wtiles) & 15) != 0) return false;
+  const int64_t lim = int64_t(1) << 31;
+  const int64_t tb = static_cast<int64_t>(a.N) * a.K / (wt == W_INT4 ? 2 : 1);
+  const int64_t xb = (static_cast<int64_t>(a.M) * a.ldx + a.K) * 2;
+  return tb < lim && xb < lim;
+}
+
+template <int WT, int SDT, int MB, int TW, int NW>
+static hipError_t launch_tiled_t(const GemmArgs& a, hipStream_t stream) {
+  const int groups = (a.N / 16 + a.tpw - 1) / a.tpw;
+  hipLaunchKernelGGL((qgemm_tiled_kernel<WT, SDT, MB, TW, NW>), dim3(groups * a.splits), dim3(64 * NW), 0, stream, a);
+  return hipGetLastError();
+}
+
+template <int WT, int SDT>
+static hipError_t launch_tiled_s(const GemmArgs& a, hipStream_t stream) {
+  const int mb = tm_mb(a.M);
+  if (mb == 1) return launch_tiled_t<WT, SDT, 1, 2, 8>(a, stream);
+  if (mb == 2) return launch_tiled_t<WT, SDT, 2, 2, 8>(a, stream);
+  if constexpr (WT == W_INT4) {
+    if (!tm_nw4()) return launch_tiled_t<WT, SDT, 4, 2, 8>(a, stream);
+  }
+  return launch_tiled_t<WT, SDT, 4, 3, 4>(a, stream);
+}
+
+hipError_t launch_tiled(int wt, const GemmArgs& a, hipStream_t stream) {
+  if (a.tpw <= 0 || a.tpw > tm_max_tpw(wt, a.M) || a.splits <= 0 || a.cps <= 0) return hipErrorInvalidValue;
+  if (wt == W_INT4) {
+    if (a.sdt == SCALE_BF16) return launch_tiled_s<W_INT4, SCALE_BF16>(a, stream);
+    if (a.sdt == SCALE_F16) return launch_tiled_s<W_INT4, SCALE_F16>(a, stream);
+    return launch_tiled_s<W_INT4, SCALE_F32>(a, stream);
+  }
+  // FP8 reads its scale dtype at run time (one scale per tile and chunk).
+  return launch_tiled_s<W_FP8, SCALE_F32>(a, stream);
+}
+
+}  // namespace hsq

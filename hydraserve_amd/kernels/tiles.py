@@ -1,15 +1,19 @@
 """Load-time tiled copies of quantized weights (a kernel-native layout).
 
 The checkpoint layouts keep each weight row contiguous (packed INT4 [N, K/8]
-int32, E4M3 [N, K] bytes).  The block-major decode kernel reads a 16-row
-block one 128-wide K chunk at a time: 16 rows x 64 bytes (INT4) per load
-instruction, i.e. sixteen 64-byte pieces 2.5-8.5 KB apart.  The tiled copy
+int32, E4M3 [N, K] bytes).  The tiled decode kernel reads 16-row blocks one
+128-wide K chunk at a time: from the row-major layout that would be 16 rows x
+64 bytes (INT4) per load instruction, i.e. sixteen 64-byte pieces 2.5-8.5 KB
+apart.  The tiled copy
 stores those 16 row pieces contiguously (tile (t, c) = rows 16t..16t+15 of
 chunk c, 1 KiB INT4 / 2 KiB FP8), so the same load instruction reads one
-contiguous KiB; on MI355X a streaming probe of the gate_up weight went from
+contiguous KiB (INT4 words also pair their nibbles: nibble i < 4 holds K
+offset 2i, nibble i + 4 holds 2i + 1, the order the tiled kernel's operand
+unpack wants); on MI355X a streaming probe of the gate_up weight went from
 ~3.6 to ~5.3 TB/s with this layout.  The copy is made once, at load time, and
-the row-major tensors stay in the weight (every other kernel reads them); the
-values are not changed (tests check the round trip and the GEMM results).
+the row-major tensors stay in the weight (every other kernel reads them, and
+the tiled kernel only takes activations of at most 64 rows); the values are
+not changed (tests check the round trip and the GEMM results).
 
 TiledInt4Weight / TiledFP8Weight are the reference's dataclasses with one
 more field, so every caller that reads the reference's fields keeps working.
@@ -33,18 +37,34 @@ class TiledFP8Weight(BlockScaledFP8Weight):
     tiles: Any = None  # uint8 [N/16, K/128, 16, 128]
 
 
+def _pair_nibbles(words, inverse: bool = False):
+    """Reorder the nibbles of int32 words: nibble 2i (K offset 2i) goes to
+    position i and nibble 2i+1 to position i+4, so that one mask of
+    0x000F000F picks two consecutive-K weights (``inverse``: back)."""
+    import torch
+
+    u = words.to(torch.int64) & 0xFFFFFFFF
+    out = torch.zeros_like(u)
+    for i in range(8):
+        dst = i // 2 + 4 * (i % 2)
+        src, to = (dst, i) if inverse else (i, dst)
+        out |= ((u >> (4 * src)) & 0xF) << (4 * to)
+    out = torch.where(out >= 2**31, out - 2**32, out)
+    return out.to(torch.int32)
+
+
 def tile_int4_weight(weight: PackedInt4Weight) -> TiledInt4Weight:
     n, k = weight.original_shape
     if n % 16 or k % 128 or weight.group_size != 128:
         raise ValueError("INT4 tiles need N % 16 == 0, K % 128 == 0 and group_size 128")
     p = weight.packed[:n, : k // 8]
-    tiles = p.reshape(n // 16, 16, k // 128, 16).permute(0, 2, 1, 3).contiguous()
+    tiles = _pair_nibbles(p.reshape(n // 16, 16, k // 128, 16).permute(0, 2, 1, 3)).contiguous()
     return TiledInt4Weight(weight.packed, weight.scale, weight.zero_point, weight.original_shape, weight.group_size, tiles)
 
 
 def untile_int4(tiles, n: int, k: int):
     """Row-major packed words [N, K/8] from the tiles (inverse of the layout)."""
-    return tiles.permute(0, 2, 1, 3).reshape(n, k // 8)
+    return _pair_nibbles(tiles, inverse=True).permute(0, 2, 1, 3).reshape(n, k // 8)
 
 
 def tile_fp8_weight(weight: BlockScaledFP8Weight) -> TiledFP8Weight:

@@ -259,8 +259,13 @@ def test_tiled_copies_round_trip_and_are_dropped_by_fuse_split():
     assert isinstance(t, TiledInt4Weight) and isinstance(t, PackedInt4Weight)
     assert t.tiles.shape == (3, 3, 16, 16)
     assert torch.equal(untile_int4(t.tiles, n, k), w.packed)
-    # tile (1, 2) = rows 16..31, words 32..47
-    assert torch.equal(t.tiles[1, 2], w.packed[16:32, 32:48])
+    # tile (1, 2) = rows 16..31, words 32..47, nibbles paired: K offset i of a
+    # word sits at nibble i/2 (even i) or 4 + i/2 (odd i)
+    src = w.packed[16:32, 32:48].to(torch.int64) & 0xFFFFFFFF
+    dst = t.tiles[1, 2].to(torch.int64) & 0xFFFFFFFF
+    for i in range(8):
+        pos = i // 2 if i % 2 == 0 else 4 + i // 2
+        assert torch.equal((src >> (4 * i)) & 15, (dst >> (4 * pos)) & 15)
     f = BlockScaledFP8Weight(
         torch.randint(0, 120, (32, 256), generator=g, dtype=torch.uint8).view(torch.float8_e4m3fn),
         torch.ones(1, 2), (32, 256),

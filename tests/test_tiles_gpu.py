@@ -1,9 +1,12 @@
 """Load-time tiled weight copies (hydraserve_amd/kernels/tiles.py) read by the
-block-major decode kernel (hs_int4_gemm_tiled / hs_fp8_gemm_tiled), against
-the oracle with the bars of tests/test_gemm_gpu.py: every M the kernel takes
-(1..16), partitions of whole 16-row tiles, all scale dtypes, the full gate_up
-shape, and shapes the kernel does not take (which fall back to the row-major
-weight in the same call)."""
+tiled decode kernel (hs_int4_gemm_tiled / hs_fp8_gemm_tiled,
+csrc/qgemm_tiled.hip), against the oracle with the bars of
+tests/test_gemm_gpu.py: every row-block count (1..64 rows, partial blocks),
+the group rewrite (<= 32 rows) and exact dequantisation (33..64 rows), all
+scale dtypes, tile groups with waves of 0..2 tiles, K split across
+workgroups (settled partials) with chunk counts that leave a ring remainder,
+the full BASELINE shapes, and shapes the kernel does not take (which fall
+back to the row-major weight in the same call)."""
 
 from __future__ import annotations
 
@@ -13,14 +16,15 @@ import torch
 
 import hydraserve_amd as hs
 from hydraserve_amd.kernels import tile_fp8_weight, tile_int4_weight
+from oracle import quant_oracle as qo
 
 from . import test_gemm_gpu as tg
 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("m", [1, 2, 4, 8, 16, 17, 64, 300])
-@pytest.mark.parametrize("n,k", [(4096, 1024), (2064, 2048)])
+@pytest.mark.parametrize("m", [1, 2, 4, 5, 8, 16, 17, 33, 37, 64, 300])
+@pytest.mark.parametrize("n,k", [(4096, 1024), (2064, 2048), (64, 384)])
 def test_int4_tiled_matches_oracle(m, n, k):
     dev = tg._cuda()
     rng = np.random.default_rng(31 * m + n)
@@ -30,16 +34,17 @@ def test_int4_tiled_matches_oracle(m, n, k):
     tg.assert_gemm_close(y, tg.int4_ref(xb, packed, scale, zero, n, k), what=f"tiled int4 {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("m", [8, 64])
 @pytest.mark.parametrize("sdt", [torch.float16, torch.float32])
-def test_int4_tiled_other_scale_dtypes(sdt):
+def test_int4_tiled_other_scale_dtypes(sdt, m):
     dev = tg._cuda()
-    rng = np.random.default_rng(77)
-    m, n, k = 4, 2048, 2048
+    rng = np.random.default_rng(77 + m)
+    n, k = 2048, 2048
     w, x, xb, packed, scale, zero, _ = tg.int4_case(rng, m, n, k, dev, sdt)
     tg.assert_gemm_close(hs.awq_linear(x, tile_int4_weight(w)), tg.int4_ref(xb, packed, scale, zero, n, k))
 
 
-@pytest.mark.parametrize("m", [1, 16, 64])
+@pytest.mark.parametrize("m", [1, 16, 33, 64])
 @pytest.mark.parametrize("sdt", [torch.float32, torch.bfloat16])
 def test_fp8_tiled_matches_oracle(m, sdt):
     dev = tg._cuda()
@@ -49,29 +54,73 @@ def test_fp8_tiled_matches_oracle(m, sdt):
     tg.assert_gemm_close(hs.fp8_linear(x, tile_fp8_weight(w)), tg.fp8_ref(xb, data, scale, n, k), what=f"tiled fp8 {m}")
 
 
-@pytest.mark.parametrize("m", [1, 4, 16])
-def test_int4_tiled_gate_up_full_shape(m):
-    dev = tg._cuda()
-    n, k = 34816, 5120
-    g = torch.Generator(device="cpu").manual_seed(700 + m)
+def _int4_full(n, k, m, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
     packed = torch.randint(-(2**31), 2**31 - 1, (n, k // 8), generator=g, dtype=torch.int32)
     zero = torch.randint(-(2**31), 2**31 - 1, (n // 8, k // 128), generator=g, dtype=torch.int32)
     scale = (torch.rand(n, k // 128, generator=g) * 9e-3 + 1e-3).to(torch.bfloat16)
     x = torch.randn(m, k, generator=g).to(torch.bfloat16)
-    w = hs.PackedInt4Weight(packed.to(dev), scale.to(dev), zero.to(dev), (n, k))
-    y = hs.awq_linear(x.to(dev), tile_int4_weight(w)).cpu()
-    y0 = hs.awq_linear(x.to(dev), w).cpu()
-    cols = tg._tile_columns(n, m)
-    from oracle import quant_oracle as qo
+    return packed, zero, scale, x
 
+
+def _int4_sampled_ref(packed, zero, scale, x, n, k, cols):
     zp = qo.unpack_zero_points(zero.numpy(), n)[cols].astype(np.int32)
     q = qo.unpack_int4_rows(packed.numpy()[cols], k).astype(np.int32)
     s = scale.float().numpy()[cols]
     gi = np.arange(k) // 128
-    w_exact = (q - zp[:, gi]).astype(np.float64) * s[:, gi]
     wd = qo.bf16_bits_to_f32(qo.f32_to_bf16_bits((q - zp[:, gi]).astype(np.float32) * s[:, gi]))
     ref = qo.gemm_f64(x.float().numpy(), wd).view(tg.RefArray)
-    ref.exact = x.float().numpy().astype(np.float64) @ w_exact.T
-    tg.assert_gemm_close(y[:, cols], ref, what=f"tiled gate_up M={m}")
-    # same per-row arithmetic as the row-major path: identical bits
-    assert torch.equal(y.view(torch.int16), y0.view(torch.int16))
+    ref.exact = x.float().numpy().astype(np.float64) @ ((q - zp[:, gi]).astype(np.float64) * s[:, gi]).T
+    return ref
+
+
+@pytest.mark.parametrize("m", [1, 8, 16, 32, 64])
+@pytest.mark.parametrize(
+    "n,k", [(34816, 5120), (5120, 17408), (10240, 5120), (5120, 8192), (12288, 5120), (4096, 4096)]
+)
+def test_int4_tiled_baseline_shapes(m, n, k):
+    """Every BASELINE decode shape through the tiled copy: one column in every
+    16-row tile plus the edges of every 256-wide block (tg._tile_columns)."""
+    dev = tg._cuda()
+    packed, zero, scale, x = _int4_full(n, k, m, 700 + m + n)
+    w = hs.PackedInt4Weight(packed.to(dev), scale.to(dev), zero.to(dev), (n, k))
+    y = hs.awq_linear(x.to(dev), tile_int4_weight(w)).cpu()
+    cols = tg._tile_columns(n, m)
+    tg.assert_gemm_close(y[:, cols], _int4_sampled_ref(packed, zero, scale, x, n, k, cols),
+                         what=f"tiled {n}x{k} M={m}")
+
+
+@pytest.mark.parametrize("m", [1, 16, 64])
+@pytest.mark.parametrize("n,k", [(34816, 5120), (5120, 17408)])
+def test_fp8_tiled_baseline_shapes(m, n, k):
+    dev = tg._cuda()
+    g = torch.Generator(device="cpu").manual_seed(m + n + 11)
+    data = torch.randint(0, 256, (n, k), generator=g, dtype=torch.int32).to(torch.uint8)
+    data[(data & 0x7F) == 0x7F] = 0x00
+    scale = torch.rand((n + 127) // 128, (k + 127) // 128, generator=g) * 0.099 + 0.001
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = hs.BlockScaledFP8Weight(data.to(dev).view(torch.float8_e4m3fn), scale.to(dev), (n, k))
+    y = hs.fp8_linear(x.to(dev), tile_fp8_weight(w)).cpu()
+    cols = tg._tile_columns(n, m)
+    wd = qo.decode_e4m3fn(data.numpy()[cols]) * scale.numpy()[(cols // 128)][:, np.arange(k) // 128]
+    ref = qo.gemm_f64(x.float().numpy(), wd.astype(np.float32))
+    tg.assert_gemm_close(y[:, cols], ref, what=f"tiled fp8 {n}x{k} M={m}")
+
+
+@pytest.mark.parametrize("m", [16, 64])
+def test_tiled_and_row_major_agree_and_replay_bitwise(m):
+    """The tiled call agrees with the row-major call on the same weight within
+    the output bar, and repeated tiled calls (split-K settles included) give
+    identical bits."""
+    dev = tg._cuda()
+    n, k = 5120, 17408
+    packed, zero, scale, x = _int4_full(n, k, m, 4242 + m)
+    w = hs.PackedInt4Weight(packed.to(dev), scale.to(dev), zero.to(dev), (n, k))
+    wt = tile_int4_weight(w)
+    xd = x.to(dev)
+    y0 = hs.awq_linear(xd, w).float()
+    y1 = hs.awq_linear(xd, wt)
+    y2 = hs.awq_linear(xd, wt)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    diff = (y1.float() - y0).abs().max().item() / y0.abs().max().item()
+    assert diff < 1e-2, diff
