@@ -5,7 +5,11 @@
 Headline workload: INT4 group-128 asymmetric decode GEMMs,
 M in {1, 4, 16, 64} x {gate_up 5120->34816, down 17408->5120}.  One "step" is
 one pass over those 8 GEMMs through the product entry point
-(hydraserve_amd.awq_linear -> C ABI -> HIP).  Inputs are synthetic and
+(hydraserve_amd.awq_linear -> C ABI -> HIP), on weights as the loader leaves
+them (`--layout tiled`, the default: the checkpoint's packed tensors plus the
+load-time tiled copy that load_linear_weights(tile=True) adds, read by the
+tiled decode kernel from 5 rows; `--layout row-major`: the checkpoint tensors
+alone).  `value_row_major` is the same step on the checkpoint tensors alone.  Inputs are synthetic and
 resident in HBM before timing; weights rotate over several independent copies
 (> 256 MB MALL) so every GEMM streams its weights from HBM.  W eager warmup
 steps run first; then exactly K steps are captured in one HIP graph (as the
@@ -91,15 +95,16 @@ def make_fp8(torch, n, k, copies, gen, dev):
 # counters read for a 512 MiB copy: FETCH x2.0, WRITE x1.0.  Kept beside the
 # summaries under profiles/; shapes not listed report null.
 PMC_TRAFFIC_KIB = {
-    ("int4", "gate_up", 64): (69799.2, 28954.0),
-    ("int4", "down", 64): (36461.5, 9866.2),
-    ("int4", "down", 16): (26201.5, 1452.5),
+    ("int4", "gate_up", 64, "row-major"): (69799.2, 28954.0),
+    ("int4", "down", 64, "row-major"): (36461.5, 9866.2),
+    ("int4", "down", 16, "row-major"): (26201.5, 1452.5),
+    ("int4", "gate_up", 64, "tiled"): (48342.6, 4352.05),
 }
 FETCH_CAL, WRITE_CAL = 2.0, 1.0
 
 
-def pmc_traffic(kind, name, m):
-    kib = PMC_TRAFFIC_KIB.get((kind, name, m))
+def pmc_traffic(kind, name, m, layout="row-major"):
+    kib = PMC_TRAFFIC_KIB.get((kind, name, m, layout))
     if kib is None:
         return None
     return int((kib[0] * FETCH_CAL + kib[1] * WRITE_CAL) * 1024)
@@ -271,10 +276,19 @@ ALL_CONFIGS = [
 ]
 
 
-def measure_all(torch, gen, dev, headline):
-    """One timed entry per (config, shape, M): graphs of back-to-back launches
-    over rotated weight copies, HIP events around the replays.  `headline`:
-    the config-1 entries already measured."""
+def tiled(kind, ws):
+    """The load-time tiled copies of a list of weights (kernels/tiles.py)."""
+    from hydraserve_amd.kernels import tile_fp8_weight, tile_int4_weight
+
+    return [tile_int4_weight(w) if kind == "int4" else tile_fp8_weight(w) for w in ws]
+
+
+def measure_all(torch, gen, dev, headline, layout):
+    """One timed entry per (config, shape, M, layout): graphs of back-to-back
+    launches over rotated weight copies, HIP events around the replays.
+    Decode rows (M <= 64) are timed on both weight layouts, prefill rows on the
+    checkpoint tensors (the prefill kernels read those in either layout).
+    `headline`: the config-1 entries already measured."""
     out = []
     for cfg, kind, name, m_list in ALL_CONFIGS:
         n, k = SHAPES[name]
@@ -282,20 +296,28 @@ def measure_all(torch, gen, dev, headline):
         per_copy = int4_bytes(n, k) if kind == "int4" else fp8_bytes(n, k)
         copies = copies_for(per_copy)
         ws = make(torch, n, k, copies, gen, dev)
+        wt = tiled(kind, ws) if min(m_list) <= 64 else None
         for m in m_list:
             x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
-            c = Case(kind, name, n, k, m, ws, x)
-            reps = 10 if m <= 64 else 4
-            ms, _ = graph_time_ms(torch, c.call, reps, 2 * copies)
-            r = c.report(ms)
-            r["config"] = cfg
-            out.append(r)
-            print(json.dumps(r), file=sys.stderr, flush=True)
-        del ws
+            for lay, wl in (("row-major", ws), ("tiled", wt)):
+                if lay == "tiled" and m > 64:
+                    continue
+                c = Case(kind, name, n, k, m, wl, x)
+                reps = 10 if m <= 64 else 4
+                ms, _ = graph_time_ms(torch, c.call, reps, 2 * copies)
+                r = c.report(ms)
+                r["config"] = cfg
+                r["layout"] = lay
+                out.append(r)
+                print(json.dumps(r), file=sys.stderr, flush=True)
+        del ws, wt
         torch.cuda.empty_cache()
-    # config 4: summed latency of one decoder layer's projections
+    # config 4: summed latency of one decoder layer's projections (decode rows
+    # on the --layout weights, prefill rows on the checkpoint tensors)
     layer = {}
     for r in headline + out:
+        if r["M"] <= 64 and r.get("layout", layout) != layout:
+            continue
         if r["kind"] == "int4" and r["shape"] in ("qkv", "o_proj", "gdn_in", "gate_up", "down") and r["M"] in (64, 1024):
             layer.setdefault(r["M"], []).append(r["us"])
     c4 = {str(m): {"us": round(sum(v), 2), "linears": len(v)} for m, v in sorted(layer.items())}
@@ -361,9 +383,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--headline-only", action="store_true", help="skip the per-config entries")
     ap.add_argument("--sweep-json", metavar="PATH", help="also write the whole result there")
+    ap.add_argument("--layout", choices=("tiled", "row-major"), default="tiled",
+                    help="weights as loaded: checkpoint tensors plus the load-time tiled copy (default), or alone")
     ap.add_argument("--profile", metavar="KIND:SHAPE:M",
-                    help="eager launches of one GEMM (e.g. int4:gate_up:64; int4silu:gate_up:M for the fused "
-                    "SiLU-and-mul store) plus a plain copy kernel of "
+                    help="eager launches of one GEMM (e.g. int4:gate_up:64; int4t / fp8t for the tiled copy; "
+                    "int4silu:gate_up:M for the fused SiLU-and-mul store) plus a plain copy kernel of "
                     "known size, for rocprofv3 counter passes; prints one JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -393,53 +417,63 @@ def main():
     per_copy = sum(int4_bytes(n, k) for n, k in shapes.values())
     copies = copies_for(per_copy)
     weights = {name: make_int4(torch, n, k, copies, gen, dev) for name, (n, k) in shapes.items()}
+    weights_t = {name: tiled("int4", ws) for name, ws in weights.items()}
     xs = {(name, m): torch.randn(m, shapes[name][1], generator=gen, device=dev).to(torch.bfloat16)
           for name in shapes for m in ms_list}
-    cases = [Case("int4", name, *shapes[name], m, weights[name], xs[(name, m)]) for m in ms_list for name in shapes]
-
-    def step(i):
-        for c in cases:
-            c.call(i)
-
-    # W eager warmup steps, then one graph of exactly K steps (step i on
-    # weight copy i mod copies), replayed once untimed and once timed.
     steps = max(1, args.steps)
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        step(0)
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for i in range(steps):
-            step(i)
-    g.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    g.replay()
-    end.record()
-    torch.cuda.synchronize()
-    t_ms = start.elapsed_time(end) / steps
-    del g
-    step_bytes = sum(c.wbytes for c in cases)
-    step_flops = sum(c.flops for c in cases)
-    value = step_bytes / (t_ms * 1e-3) / 1e9
 
-    # per-kernel times: graphs of back-to-back launches of one GEMM
+    def timed_steps(cases):
+        """W eager warmup steps, then one graph of exactly K steps (step i on
+        weight copy i mod copies), replayed once untimed and once timed; ms per step."""
+
+        def step(i):
+            for c in cases:
+                c.call(i)
+
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step(0)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                step(i)
+        g.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        g.replay()
+        end.record()
+        torch.cuda.synchronize()
+        del g
+        return start.elapsed_time(end) / steps
+
+    cases = {lay: [Case("int4", name, *shapes[name], m, wd[name], xs[(name, m)]) for m in ms_list for name in shapes]
+             for lay, wd in (("tiled", weights_t), ("row-major", weights))}
+    t_ms_by = {lay: timed_steps(cases[lay]) for lay in ("row-major", "tiled")}
+    t_ms = t_ms_by[args.layout]
+    step_bytes = sum(c.wbytes for c in cases[args.layout])
+    step_flops = sum(c.flops for c in cases[args.layout])
+    value = step_bytes / (t_ms * 1e-3) / 1e9
+    value_rm = step_bytes / (t_ms_by["row-major"] * 1e-3) / 1e9
+
+    # per-kernel times: graphs of back-to-back launches of one GEMM, both layouts
     per = []
-    for c in cases:
-        ms, _ = graph_time_ms(torch, c.call, 10, 2 * copies)
-        r = c.report(ms)
-        r["config"] = "c1"
-        per.append((c, ms, r))
-    del weights, cases, xs
+    for lay in ("row-major", "tiled"):
+        for c in cases[lay]:
+            ms, _ = graph_time_ms(torch, c.call, 10, 2 * copies)
+            r = c.report(ms)
+            r["config"] = "c1"
+            r["layout"] = lay
+            per.append((c, ms, r))
+    del weights, weights_t, cases, xs
     torch.cuda.empty_cache()
-    dom_c, dom_ms, dom_r = max(per, key=lambda t: t[1])
+    dom_c, dom_ms, dom_r = max((t for t in per if t[2]["layout"] == args.layout), key=lambda t: t[1])
     ceiling = hbm_ceiling(torch, dev)
     roofline = {
         "bound": "hbm",
@@ -447,8 +481,8 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(dom_r["weight_GBps"] / HBM_PEAK_GBS, 4),
-        "traffic": pmc_traffic("int4", dom_c.name, dom_c.m),
-        "kernel": f"INT4 decode {dom_c.name} M={dom_c.m} ({dom_c.n}x{dom_c.k})",
+        "traffic": pmc_traffic("int4", dom_c.name, dom_c.m, args.layout),
+        "kernel": f"INT4 decode {dom_c.name} M={dom_c.m} ({dom_c.n}x{dom_c.k}), {args.layout} weights",
         "bytes_per_launch": dom_c.wbytes,
         "us_per_launch": dom_r["us"],
         "measured_ceiling_GBps": ceiling["GBps"],
@@ -460,6 +494,8 @@ def main():
         "metric": "INT4/FP8 GEMM TFLOP/s + weight HBM GB/s (% roofline), M=1..2048, 1 MI355X",
         "value": round(value, 1),
         "unit": "GB/s",
+        "value_row_major": round(value_rm, 1),
+        "ms_per_step_row_major": round(t_ms_by["row-major"], 4),
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
@@ -473,6 +509,7 @@ def main():
         "config": {
             "workload": "config 1: INT4 g128 asymmetric decode GEMMs, M in {1,4,16,64} x "
             "{gate_up 5120->34816, down 17408->5120}, 8 GEMMs per step",
+            "layout": args.layout,
             "weight_bytes_per_step": step_bytes,
             "tflops": round(step_flops / (t_ms * 1e-3) / 1e12, 3),
             "weight_copies": copies,
@@ -483,7 +520,7 @@ def main():
     }
 
     if not args.headline_only:
-        entries, c4 = measure_all(torch, gen, dev, result["per_shape"])
+        entries, c4 = measure_all(torch, gen, dev, result["per_shape"], args.layout)
         result["per_shape"] += entries
         result["config4_layer"] = c4
         prefill = [r for r in entries if r["bound"] == "mfma"]
@@ -532,12 +569,18 @@ def profile(torch, gen, dev, spec, launches):
     m = int(m)
     # kind "int4silu": gate_up with the fused SiLU-and-mul store, on weights
     # interleaved at load time (awq_gate_up_silu_mul)
+    # kind "int4t" / "fp8t": the load-time tiled copy (tiled decode kernel)
     fused = kind == "int4silu"
     if fused:
         kind = "int4"
+    tiled_w = kind in ("int4t", "fp8t")
+    if tiled_w:
+        kind = kind[:-1]
     make = make_int4 if kind == "int4" else make_fp8
     per_copy = int4_bytes(n, k) if kind == "int4" else fp8_bytes(n, k)
     ws = make(torch, n, k, copies_for(per_copy), gen, dev)
+    if tiled_w:
+        ws = tiled(kind, ws)
     x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
     if fused:
         from hydraserve_amd.kernels import awq_gate_up_silu_mul, interleave_gate_up

@@ -210,7 +210,10 @@ TmPlan tm_plan(int wt, int M, int N, int K) {
     const int tw = (tpw + 3) / 4;  // tiles per SIMD
     const double mem = tpw * tb + 0.5 * mb * 4096.0;
     const double cmp = tw * comp;
-    const double est = waves_per_cu * cps * (mem > cmp ? mem : cmp) + (S > 1 ? 40000.0 : 0.0);
+    // a split group settles after its last K range: partial stores, the
+    // arrival, then coherent loads of four contributors per round trip
+    const double settle = S > 1 ? 30000.0 + 20000.0 * ((S + 3) / 4) : 0.0;
+    const double est = waves_per_cu * cps * (mem > cmp ? mem : cmp) + settle;
     if (est < best_est) {
       best_est = est;
       best.tpw = tpw;
@@ -228,9 +231,13 @@ TmPlan tm_plan(int wt, int M, int N, int K) {
 // 1..4 rows stays on the row-major block-major / row-partitioned kernels
 // (gate_up M=4: 25.5 vs 27.9 us; down M=1: 17.2 vs 21.0 us); from 5 rows and
 // for FP8 at every row count the tiled kernel is faster.
-bool tm_min_ok(int wt, int M) {
+// Small weights stay row-major too: the tiled kernel's ring fill and drain
+// cost ~5 us a launch (INT4 4096x4096 at M=8: 9.2 vs 7.7 us).
+bool tm_min_ok(int wt, int M, int N, int K) {
   const Tuning& tn = tuning();
-  return !tn.tm_off && M >= (tn.tm_min_m > 0 ? tn.tm_min_m : (wt == W_INT4 ? 5 : 1));
+  if (tn.tm_off) return false;
+  if (tn.tm_min_m > 0) return M >= tn.tm_min_m;
+  return M >= (wt == W_INT4 ? 5 : 1) && static_cast<int64_t>(N) * K >= (int64_t{32} << 20);
 }
 
 // Register-streamed decode kernel layouts: S 16-row blocks per wave, NB
@@ -404,7 +411,7 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   const Tuning& tn = tuning();
   // Tiled weight copy: the tiled decode kernel (contiguous KiB weight loads);
   // every other kernel reads the row-major weight.
-  if (a.wtiles != nullptr && tm_min_ok(wt, a.M) && tiled_ok(a, wt)) {
+  if (a.wtiles != nullptr && tm_min_ok(wt, a.M, a.N, a.K) && tiled_ok(a, wt)) {
     const TmPlan tp = tm_plan(wt, a.M, a.N, a.K);
     if (tp.P > 0) {
       if (tp.splits > 1 && (workspace == nullptr || workspace_bytes < tp.ws_bytes)) return HS_EWORKSPACE;

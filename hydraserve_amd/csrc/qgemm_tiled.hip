@@ -437,17 +437,27 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
   for (int i = 0; i < TW; ++i)
 #pragma unroll
     for (int b = 0; b < MB; ++b) sum[i][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int q = 0; q < a.splits; ++q) {
-    const int pp = g * a.splits + q;
-    f32x4_t v[TW][MB];
+  // Contributors in K-range order, up to four with all loads in flight
+  // (every load is a coherent round trip); a slot past the last contributor
+  // re-reads the last one and adds zero.
+  for (int q0 = 0; q0 < a.splits; q0 += 4) {
+    f32x4_t v[4][TW][MB];
 #pragma unroll
-    for (int i = 0; i < TW; ++i)
+    for (int u = 0; u < 4; ++u) {
+      const int q = q0 + u < a.splits ? q0 + u : a.splits - 1;
 #pragma unroll
-      for (int b = 0; b < MB; ++b) v[i][b] = load_partial4(pr, poff(pp, i, b));
+      for (int i = 0; i < TW; ++i)
 #pragma unroll
-    for (int i = 0; i < TW; ++i)
+        for (int b = 0; b < MB; ++b) v[u][i][b] = load_partial4(pr, poff(g * a.splits + q, i, b));
+    }
 #pragma unroll
-      for (int b = 0; b < MB; ++b) sum[i][b] += v[i][b];
+    for (int u = 0; u < 4; ++u) {
+      const float keep = q0 + u < a.splits ? 1.0f : 0.0f;
+#pragma unroll
+      for (int i = 0; i < TW; ++i)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) sum[i][b] += v[u][i][b] * keep;
+    }
   }
 #pragma unroll
   for (int i = 0; i < TW; ++i) {

@@ -1,0 +1,58 @@
+"""Child process of tests/test_tiles_gpu.py: parity of the tiled decode
+kernel (csrc/qgemm_tiled.hip) on small shapes.
+
+By default the plan sends small weights (N*K below 32M) and INT4 at 1..4 rows
+to the row-major kernels; this child runs with HS_TM_MIN_M=1 (read once per
+process), so every case below goes through the tiled kernel: every row-block
+count (1..64 rows, partial blocks), waves holding 0..2 tiles (N = 64: four
+tiles), K ranges split across workgroups, all scale dtypes.  The checks are
+those of tests/test_gemm_gpu.py, plus a bit-identical second call.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from tests import test_gemm_gpu as tg
+
+import hydraserve_amd as hs
+from hydraserve_amd.kernels import tile_fp8_weight, tile_int4_weight
+
+# (kind, M, N, K, scale dtype)
+CASES = (
+    [("int4", m, n, k, torch.bfloat16) for m in (1, 2, 4, 5, 8, 16, 17, 33, 37, 64)
+     for n, k in ((4096, 1024), (2064, 2048), (64, 384))]
+    + [("int4", m, 2048, 2048, sdt) for m in (8, 64) for sdt in (torch.float16, torch.float32)]
+    + [("fp8", m, 4096, 2048, sdt) for m in (1, 16, 33, 64) for sdt in (torch.float32, torch.bfloat16)]
+    + [("fp8", m, 272, 1024, torch.float16) for m in (3, 40)]
+)
+
+
+def main() -> int:
+    dev = torch.device("cuda", 0)
+    for i, (kind, m, n, k, sdt) in enumerate(CASES):
+        rng = np.random.default_rng(31 * m + n + i)
+        what = f"tiled {kind} M={m} N={n} K={k} {sdt}"
+        print(what, flush=True)
+        if kind == "int4":
+            w, x, xb, packed, scale, zero, _ = tg.int4_case(rng, m, n, k, dev, sdt)
+            wt = tile_int4_weight(w)
+            y = hs.awq_linear(x, wt)
+            y2 = hs.awq_linear(x, wt)
+            ref = tg.int4_ref(xb, packed, scale, zero, n, k)
+        else:
+            w, x, xb, data, scale = tg.fp8_case(rng, m, n, k, dev, sdt)
+            wt = tile_fp8_weight(w)
+            y = hs.fp8_linear(x, wt)
+            y2 = hs.fp8_linear(x, wt)
+            ref = tg.fp8_ref(xb, data, scale, n, k)
+        torch.cuda.synchronize()
+        tg.assert_gemm_close(y, ref, what=what)
+        assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), what
+    print("ok", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
