@@ -198,7 +198,8 @@ TmPlan tm_plan(int wt, int M, int N, int K) {
   for (int s0 : cand) {
     if (tn.tm_s > 0 && s0 != tn.tm_s) continue;
     if (s0 > NC) break;
-    const int cps = static_cast<int>(cdiv(NC, s0));
+    // INT4 K ranges start at multiples of 8 chunks (the kernel's scale rounds)
+    const int cps = wt == W_INT4 ? static_cast<int>(8 * cdiv(cdiv(NC, s0), 8)) : static_cast<int>(cdiv(NC, s0));
     const int S = static_cast<int>(cdiv(NC, cps));
     int tpw = tn.tm_tpw > 0 ? tn.tm_tpw : static_cast<int>(cdiv(NT * S, cus));
     if (tpw < 1) tpw = 1;
@@ -428,7 +429,11 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   // streaming kernel over row halves measured faster (INT4 / FP8 down
   // 17408->5120 at M=256: 102 / 100 us against 108 / 111 us; M=160: 80 vs
   // 106 us).  Sequential on the stream, so they share the workspace.
-  if (!tn.row_split_off && a.M > 128 && a.M <= 256 && a.N < a.K && a.silu_mul == 0) {
+  // With a tiled weight copy and at most 64 rows in the upper half, wide
+  // outputs split too: the upper half goes to the tiled decode kernel (INT4 /
+  // FP8 qkv 12288x5120 at M=192: 60 / 64 us against 73 / 76 us in one pass).
+  if (!tn.row_split_off && a.M > 128 && a.M <= 256 && (a.N < a.K || (a.wtiles != nullptr && a.M <= 192)) &&
+      a.silu_mul == 0) {
     GemmArgs lo = a, hi = a;
     lo.M = 128;
     hi.M = a.M - 128;
@@ -595,7 +600,7 @@ int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
     best = b > best ? b : best;
   }
   // the two row halves of the narrow-output split at 129..256 rows
-  if (M > 128 && M <= 256 && N < K) {
+  if (M > 128 && M <= 256 && (N < K || M <= 192)) {
     const int64_t lo = hs_gemm_workspace_bytes(kind, 128, N, K), hi = hs_gemm_workspace_bytes(kind, M - 128, N, K);
     best = lo > best ? lo : best;
     best = hi > best ? hi : best;

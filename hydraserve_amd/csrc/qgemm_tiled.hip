@@ -75,15 +75,22 @@ struct Tm {
   static_assert(D % R == 0 && R < D, "X rounds tile the ring");
   static constexpr int XR = R * XB;                      // X bytes of a round
   static constexpr int LXR = (R * XI + NW - 1) / NW;     // X loads per wave per round
-  static constexpr int SB = NW * 256;
-  static constexpr int ZB = WT == W_INT4 ? NW * 256 : 0;
-  static constexpr int SLOTB = SB + ZB;
-  static_assert(2 * XR + D * SLOTB + 1024 + 256 <= kTmLds, "LDS");
+  // FP8: the chunk's scales (one per tile) in each ring slot.  INT4: the
+  // scales and zero points of a whole ring round (D = 8 chunks) per wave,
+  // double-buffered by round: MSB bytes per wave, scales at 0 (two 1 KiB
+  // halves for fp32 scales, one for 16-bit ones), zero points at 2048.
+  static constexpr int SB = WT == W_INT4 ? 0 : NW * 256;
+  static constexpr int SLOTB = SB > 16 ? SB : 16;
+  static constexpr int MSB = WT == W_INT4 ? 3072 : 0;
+  static constexpr int MB2 = MSB > 0 ? 2 * NW * MSB : 16;
+  static_assert(WT != W_INT4 || D == 8, "INT4 scale rounds are ring rounds of 8 chunks");
+  static_assert(2 * XR + D * SLOTB + MB2 + 1024 + 256 <= kTmLds, "LDS");
   static constexpr int SLOT = NW * TW * MB * 256;  // floats of one workgroup's partial
 
   struct Smem {
     __attribute__((aligned(1024))) uint8_t xs[2][XR];
     __attribute__((aligned(1024))) uint8_t ring[D][SLOTB];
+    __attribute__((aligned(1024))) uint8_t meta[MB2];
     uint8_t junk[1024];  // target of the X loads that carry no data
     int flag;
   };
@@ -99,10 +106,10 @@ struct Tm {
   }
 };
 
-// Round starts (steps t = 0 mod R) among steps lo .. hi (may be negative).
-constexpr int tm_round_starts(int lo, int hi, int R) {
+// Steps t = r mod R among steps lo .. hi (may be negative).
+constexpr int tm_steps_mod(int lo, int hi, int R, int r = 0) {
   int n = 0;
-  for (int t = lo; t <= hi; ++t) n += (((t % R) + R) % R) == 0;
+  for (int t = lo; t <= hi; ++t) n += (((t % R) + R) % R) == r;
   return n;
 }
 
@@ -180,7 +187,15 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
   int64_t se0;
   if constexpr (WT == W_INT4) se0 = static_cast<int64_t>(16 * tt[li] + n) * a.lds;
   else se0 = static_cast<int64_t>((16 * tt[li]) >> 7) * a.lds;
-  const uint32_t zo0 = WT == W_INT4 ? static_cast<uint32_t>(((16 * tt[li] + n) >> 3) * a.ldz) * 4u : 0u;
+  // INT4 round loads (lane l, chunks c .. c+7 of a round at c = 0 mod 8):
+  // scales of tile li, row n, 16 bytes per lane per 16-byte half (fp32: two
+  // halves of four chunks); zero-point words of tile l/4, word row
+  // (l/2) % 2 (tile rows 8h .. 8h+7), chunks 4 (l % 2) .. +3.
+  const int zt = (lane >> 2) < TW ? (lane >> 2) : TW - 1;
+  const uint32_t so0 = WT == W_INT4 ? static_cast<uint32_t>(se0 * ses) : 0u;
+  const uint32_t zo0 = WT == W_INT4 ? static_cast<uint32_t>((2 * tt[zt] + ((lane >> 1) & 1)) * a.ldz) * 4u +
+                                          static_cast<uint32_t>(lane & 1) * 16u
+                                    : 0u;
 
   // INT4 group rewrite (128 + q as bf16, one v_and_or_b32 per two weights)
   // where the per-element correction stays cheaper than exact dequantisation.
@@ -205,7 +220,10 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
     constexpr int NTW = decltype(ntc)::value;
     constexpr int R = C::R;
     // loads per wave per chunk: scales, (INT4) zero points, weights
-    constexpr int Lc = (NTW > 0 ? 1 + (WT == W_INT4 ? 1 : 0) : 0) + NTW * LPT;
+    constexpr int Lc = (NTW > 0 && WT != W_INT4 ? 1 : 0) + NTW * LPT;
+    // INT4 round loads (scales, zero points) of a wave, issued with the
+    // weights of the round's first chunk.
+    constexpr int Lm = WT == W_INT4 && NTW > 0 ? (SDT == SCALE_F32 ? 3 : 2) : 0;
     u32x4_t W[D][NTW > 0 ? NTW : 1][LPT];  // weight ring (registers)
 
     // X of round rho (chunks rho*R ..) into X buffer rho % 2; rounds past the
@@ -223,13 +241,23 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
     // registers.)
     auto issue = [&](int J, int k) __attribute__((always_inline)) {
       if constexpr (NTW > 0) {
+        if constexpr (WT == W_INT4) {
+          if (J == 0) {
+            // the round of chunks k .. k+7 (k = 0 mod 8; unclamped: a round
+            // past the range reads bytes nobody uses)
+            uint8_t* mb = &sm.meta[0] + ((k >> 3) & 1) * (NW * C::MSB) + wave * C::MSB;
+            const uint32_t cs = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c0 + k) * ses);
+            C::dma(rs.s, mb, 16, so0, cs);
+            if constexpr (SDT == SCALE_F32) C::dma(rs.s, mb + 1024, 16, so0 + 16u, cs);
+            C::dma(rs.z, mb + 2048, 16, zo0, __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c0 + k) * 4u));
+          }
+        }
         k = k < nk ? k : nk - 1;
         const int c = c0 + k;
-        uint8_t* base = &sm.ring[J][0];
-        const uint32_t sb = static_cast<uint32_t>((se0 + c) * ses) & ~3u;
-        C::dma(rs.s, base + wave * 256, 4, sb, 0);
-        if constexpr (WT == W_INT4)
-          C::dma(rs.z, base + C::SB + wave * 256, 4, zo0 + static_cast<uint32_t>(c) * 4u, 0);
+        if constexpr (WT != W_INT4) {
+          const uint32_t sb = static_cast<uint32_t>((se0 + c) * ses) & ~3u;
+          C::dma(rs.s, &sm.ring[J][0] + wave * 256, 4, sb, 0);
+        }
         const uint32_t kw = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c) * C::TB);
 #pragma unroll
         for (int i = 0; i < NTW; ++i)
@@ -243,12 +271,25 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
       if constexpr (NTW > 0) {
         const uint8_t* xchunk = &sm.xs[(k / R) & 1][0] + (J % R) * C::XB;
         const int c = c0 + k;
-        const uint8_t* sbase = &sm.ring[J][0] + wave * 256;
         uint32_t sd[NTW], zd[NTW];
+        if constexpr (WT == W_INT4) {
+          // chunk k = J mod 8 of its round
+          const uint8_t* mb = &sm.meta[0] + ((k >> 3) & 1) * (NW * C::MSB) + wave * C::MSB;
 #pragma unroll
-        for (int i = 0; i < NTW; ++i) {
-          sd[i] = *reinterpret_cast<const uint32_t*>(sbase + (WT == W_INT4 ? (16 * i + n) * 4 : (16 * i) * 4));
-          zd[i] = WT == W_INT4 ? *reinterpret_cast<const uint32_t*>(sbase + C::SB + (16 * i + n) * 4) : 0u;
+          for (int i = 0; i < NTW; ++i) {
+            if constexpr (SDT == SCALE_F32)
+              sd[i] = *reinterpret_cast<const uint32_t*>(mb + (J >> 2) * 1024 + (16 * i + n) * 16 + (J & 3) * 4);
+            else
+              sd[i] = *reinterpret_cast<const uint16_t*>(mb + (16 * i + n) * 16 + J * 2);
+            zd[i] = *reinterpret_cast<const uint32_t*>(mb + 2048 + 16 * (4 * i + 2 * (n >> 3) + (J >> 2)) + 4 * (J & 3));
+          }
+        } else {
+          const uint8_t* sbase = &sm.ring[J][0] + wave * 256;
+#pragma unroll
+          for (int i = 0; i < NTW; ++i) {
+            sd[i] = *reinterpret_cast<const uint32_t*>(sbase + (16 * i) * 4);
+            zd[i] = 0u;
+          }
         }
         bf16x8_t A[MB][4];
 #pragma unroll
@@ -275,11 +316,10 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
         for (int i = 0; i < NTW; ++i) {
           const int t = tt[i];
           if constexpr (WT == W_INT4) {
-            const int64_t e = static_cast<int64_t>(16 * t + n) * a.lds + c;
             float s;
             if constexpr (SDT == SCALE_F32) s = __uint_as_float(sd[i]);
-            else if constexpr (SDT == SCALE_BF16) s = __uint_as_float((sd[i] >> ((e & 1) * 16)) << 16);
-            else s = __half2float(__ushort_as_half(static_cast<unsigned short>(sd[i] >> ((e & 1) * 16))));
+            else if constexpr (SDT == SCALE_BF16) s = __uint_as_float(sd[i] << 16);
+            else s = __half2float(__ushort_as_half(static_cast<unsigned short>(sd[i])));
             const uint32_t z = (zd[i] >> ((n & 7) * 4)) & 0xFu;
             if constexpr (REW) {
               // acc += s * (sum x (128+q) - (128+z) * Xg)
@@ -361,8 +401,11 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
     // it needs: chunk k's group, and at a round start also this round's X.
     auto step = [&](auto jc, int k) __attribute__((always_inline)) {
       constexpr int J = decltype(jc)::value;
-      constexpr int after_g = (D - 2) * Lc + C::LXR * tm_round_starts(J - D + 2, J - 1, R);
-      constexpr int after_x = R * Lc;
+      // (X rounds start at steps t = 0 mod R; INT4 round loads go out at
+      // steps t = 1 mod D, with the weights of chunk t + D - 1 = 0 mod D.)
+      constexpr int after_g = (D - 2) * Lc + C::LXR * tm_steps_mod(J - D + 2, J - 1, R) +
+                              Lm * tm_steps_mod(J - D + 2, J - 1, D, 1);
+      constexpr int after_x = R * Lc + Lm * tm_steps_mod(J - R, J - 1, D, 1);
       constexpr int later = (J % R == 0 && after_x < after_g) ? after_x : after_g;
       static_assert(later <= 63, "vmcnt range");
       __builtin_amdgcn_s_waitcnt((later & 15) | ((later >> 4) << 14) | 0x0F70);
@@ -493,11 +536,18 @@ int tm_max_tpw(int wt, int M) { return tm_nw(wt, M) * tm_tw(wt, M); }
 int tm_slot_floats(int wt, int M) { return tm_nw(wt, M) * tm_tw(wt, M) * tm_mb(M) * 256; }
 
 // Tiled copy present, M <= 64, N a multiple of 16, K a multiple of 128, every
-// buffer range below 2^31 bytes.
+// buffer range below 2^31 bytes; INT4 scale and zero-point rows 16-byte aligned.
 bool tiled_ok(const GemmArgs& a, int wt) {
   if (a.wtiles == nullptr || a.M <= 0 || a.M > 64 || a.N % 16 != 0 || a.K % 128 != 0 || a.silu_mul || !a.xvec)
     return false;
   if ((reinterpret_cast<uintptr_t>(a.scale) & 3) != 0 || (reinterpret_cast<uintptr_t>(a.wtiles) & 15) != 0) return false;
+  if (wt == W_INT4) {
+    // a round's scales and zero points go by 16-byte loads (chunks 8j .. 8j+7)
+    const int ses = a.sdt == SCALE_F32 ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(a.scale) & 15) != 0 || (a.lds * ses) % 16 != 0 ||
+        (reinterpret_cast<uintptr_t>(a.zero) & 15) != 0 || (a.ldz * 4) % 16 != 0)
+      return false;
+  }
   const int64_t lim = int64_t(1) << 31;
   const int64_t tb = static_cast<int64_t>(a.N) * a.K / (wt == W_INT4 ? 2 : 1);
   const int64_t xb = (static_cast<int64_t>(a.M) * a.ldx + a.K) * 2;

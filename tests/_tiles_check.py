@@ -4,7 +4,8 @@ kernel (csrc/qgemm_tiled.hip) on small shapes.
 By default the plan sends small weights (N*K below 32M) and INT4 at 1..4 rows
 to the row-major kernels; this child runs with HS_TM_MIN_M=1 (read once per
 process), so every case below goes through the tiled kernel: every row-block
-count (1..64 rows, partial blocks), waves holding 0..2 tiles (N = 64: four
+count (1..64 rows, partial blocks; 129..192 rows split into 128 row-major
+rows and a tiled rest), waves holding 0..2 tiles (N = 64: four
 tiles), K ranges split across workgroups, all scale dtypes.  The checks are
 those of tests/test_gemm_gpu.py, plus a bit-identical second call.
 """
@@ -26,6 +27,9 @@ CASES = (
     + [("int4", m, 2048, 2048, sdt) for m in (8, 64) for sdt in (torch.float16, torch.float32)]
     + [("fp8", m, 4096, 2048, sdt) for m in (1, 16, 33, 64) for sdt in (torch.float32, torch.bfloat16)]
     + [("fp8", m, 272, 1024, torch.float16) for m in (3, 40)]
+    # 129..192 rows: 128 rows row-major, the rest through the tiled kernel
+    + [("int4", 160, 4096, 1024, torch.bfloat16), ("fp8", 192, 4096, 2048, torch.float32),
+       ("int4", 190, 1024, 4096, torch.float16)]
 )
 
 

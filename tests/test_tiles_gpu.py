@@ -124,3 +124,29 @@ def test_tiled_and_row_major_agree_and_replay_bitwise(m):
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
     diff = (y1.float() - y0).abs().max().item() / y0.abs().max().item()
     assert diff < 1e-2, diff
+
+
+@pytest.mark.parametrize("kind", ["int4", "fp8"])
+def test_tiled_row_split_qkv_m192(kind):
+    """129..192 rows on a wide output with a tiled copy: 128 rows row-major and
+    the upper 64 rows through the tiled kernel, sampled columns against the
+    oracle."""
+    dev = tg._cuda()
+    n, k, m = 12288, 5120, 192
+    cols = tg._tile_columns(n, 16)
+    if kind == "int4":
+        packed, zero, scale, x = _int4_full(n, k, m, 1921)
+        w = hs.PackedInt4Weight(packed.to(dev), scale.to(dev), zero.to(dev), (n, k))
+        y = hs.awq_linear(x.to(dev), tile_int4_weight(w)).cpu()
+        ref = _int4_sampled_ref(packed, zero, scale, x, n, k, cols)
+    else:
+        g = torch.Generator(device="cpu").manual_seed(1922)
+        data = torch.randint(0, 256, (n, k), generator=g, dtype=torch.int32).to(torch.uint8)
+        data[(data & 0x7F) == 0x7F] = 0x00
+        scale = torch.rand(n // 128, k // 128, generator=g) * 0.099 + 0.001
+        x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+        w = hs.BlockScaledFP8Weight(data.to(dev).view(torch.float8_e4m3fn), scale.to(dev), (n, k))
+        y = hs.fp8_linear(x.to(dev), tile_fp8_weight(w)).cpu()
+        wd = qo.decode_e4m3fn(data.numpy()[cols]) * scale.numpy()[(cols // 128)][:, np.arange(k) // 128]
+        ref = qo.gemm_f64(x.float().numpy(), wd.astype(np.float32))
+    tg.assert_gemm_close(y[:, cols], ref, what=f"tiled split {kind} M={m}")
