@@ -198,8 +198,8 @@ TmPlan tm_plan(int wt, int M, int N, int K) {
   for (int s0 : cand) {
     if (tn.tm_s > 0 && s0 != tn.tm_s) continue;
     if (s0 > NC) break;
-    // INT4 K ranges start at multiples of 8 chunks (the kernel's scale rounds)
-    const int cps = wt == W_INT4 ? static_cast<int>(8 * cdiv(cdiv(NC, s0), 8)) : static_cast<int>(cdiv(NC, s0));
+    // INT4 K ranges start at even chunks (4-byte aligned 16-bit scale loads)
+    const int cps = wt == W_INT4 ? static_cast<int>(2 * cdiv(cdiv(NC, s0), 2)) : static_cast<int>(cdiv(NC, s0));
     const int S = static_cast<int>(cdiv(NC, cps));
     int tpw = tn.tm_tpw > 0 ? tn.tm_tpw : static_cast<int>(cdiv(NT * S, cus));
     if (tpw < 1) tpw = 1;

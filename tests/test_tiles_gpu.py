@@ -30,13 +30,18 @@ pytestmark = pytest.mark.gpu
 ROOT = Path(__file__).resolve().parents[1]
 
 
-def test_tiled_kernel_small_shapes_forced():
+@pytest.mark.parametrize("splits", [None, "3"])
+def test_tiled_kernel_small_shapes_forced(splits):
     """Small shapes forced through the tiled kernel in a child process
     (tests/_tiles_check.py, HS_TM_MIN_M=1): the plan keeps them row-major by
-    default."""
+    default.  HS_TM_S=3 forces three K ranges where the shape allows, so K
+    ranges start at chunks that are not multiples of the 8-chunk scale
+    rounds."""
     if not torch.cuda.is_available():
         pytest.skip("needs a ROCm GPU")
     env = dict(os.environ, HS_TM_MIN_M="1")
+    if splits:
+        env["HS_TM_S"] = splits
     res = subprocess.run([sys.executable, "-u", "-m", "tests._tiles_check"], cwd=ROOT, env=env,
                          capture_output=True, text=True, timeout=110)
     assert res.returncode == 0, res.stdout[-3000:] + res.stderr[-3000:]
