@@ -8,7 +8,7 @@ one pass over those 8 GEMMs through the product entry point
 (hydraserve_amd.awq_linear -> C ABI -> HIP), on weights as the loader leaves
 them (`--layout tiled`, the default: the checkpoint's packed tensors plus the
 load-time tiled copy that load_linear_weights(tile=True) adds, read by the
-tiled decode kernel from 5 rows; `--layout row-major`: the checkpoint tensors
+tiled decode kernel up to 64 rows; `--layout row-major`: the checkpoint tensors
 alone).  `value_row_major` is the same step on the checkpoint tensors alone.  Inputs are synthetic and
 resident in HBM before timing; weights rotate over several independent copies
 (> 256 MB MALL) so every GEMM streams its weights from HBM.  W eager warmup

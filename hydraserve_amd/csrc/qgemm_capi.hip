@@ -228,17 +228,18 @@ TmPlan tm_plan(int wt, int M, int N, int K) {
   return best;
 }
 
-// Measured on MI355X (gate_up 5120->34816, down 17408->5120, qkv): INT4 at
-// 1..4 rows stays on the row-major block-major / row-partitioned kernels
-// (gate_up M=4: 25.5 vs 27.9 us; down M=1: 17.2 vs 21.0 us); from 5 rows and
-// for FP8 at every row count the tiled kernel is faster.
-// Small weights stay row-major too: the tiled kernel's ring fill and drain
-// cost ~5 us a launch (INT4 4096x4096 at M=8: 9.2 vs 7.7 us).
+// Measured on MI355X (gate_up 5120->34816, down 17408->5120, qkv): with the
+// scale rounds the tiled kernel is faster at every row count for INT4 too
+// (gate_up M=1 / 4: 22.8 / 21.8 us against 28.3 / 26.2 on the row-major
+// kernels; down M=1 / 4: 16.7 / 16.7 against 19.8 / 21.5).
+// Small weights stay row-major: the tiled kernel's ring fill and drain cost
+// ~5 us a launch (INT4 4096x4096 at M=8: 9.2 vs 7.7 us).
 bool tm_min_ok(int wt, int M, int N, int K) {
   const Tuning& tn = tuning();
   if (tn.tm_off) return false;
   if (tn.tm_min_m > 0) return M >= tn.tm_min_m;
-  return M >= (wt == W_INT4 ? 5 : 1) && static_cast<int64_t>(N) * K >= (int64_t{32} << 20);
+  (void)wt;
+  return M >= 1 && static_cast<int64_t>(N) * K >= (int64_t{32} << 20);
 }
 
 // Register-streamed decode kernel layouts: S 16-row blocks per wave, NB

@@ -1,8 +1,8 @@
 """Child process of tests/test_tiles_gpu.py: parity of the tiled decode
 kernel (csrc/qgemm_tiled.hip) on small shapes.
 
-By default the plan sends small weights (N*K below 32M) and INT4 at 1..4 rows
-to the row-major kernels; this child runs with HS_TM_MIN_M=1 (read once per
+By default the plan sends small weights (N*K below 32M) to the row-major
+kernels; this child runs with HS_TM_MIN_M=1 (read once per
 process), so every case below goes through the tiled kernel: every row-block
 count (1..64 rows, partial blocks; 129..192 rows split into 128 row-major
 rows and a tiled rest), waves holding 0..2 tiles (N = 64: four

@@ -50,8 +50,8 @@ def test_tiled_kernel_small_shapes_forced(splits):
 
 @pytest.mark.parametrize("m", [1, 8, 300])
 def test_int4_tiled_weight_default_dispatch(m):
-    """A tiled weight through the default plan (row-major kernels below 5 rows,
-    for small weights and above 64 rows)."""
+    """A tiled weight through the default plan (row-major kernels for small
+    weights and above 64 rows)."""
     dev = tg._cuda()
     rng = np.random.default_rng(17 * m)
     n, k = 2064, 2048
