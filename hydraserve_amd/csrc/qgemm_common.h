@@ -26,6 +26,7 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 enum WeightKind { W_INT4 = 0, W_FP8 = 1 };
 enum ScaleDtype { SCALE_BF16 = 0, SCALE_F16 = 1, SCALE_F32 = 2 };

@@ -104,6 +104,9 @@ struct Tm {
   static __device__ __forceinline__ u32x4_t wload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
   }
+  static __device__ __forceinline__ u32x2_t wload8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+  }
 };
 
 // Steps t = r mod R among steps lo .. hi (may be negative).
@@ -113,21 +116,31 @@ constexpr int tm_steps_mod(int lo, int hi, int R, int r = 0) {
   return n;
 }
 
-template <int WT, int SDT, int MB, int TW, int NW>
+// KS (INT4, exact dequantisation): the waves pair up on the K16 steps of
+// their tiles.  Wave w takes tile set w/2 (tiles w/2, w/2 + NW/2, ...) and
+// K half w%2 (steps 2(w%2), 2(w%2)+1 of every chunk): each wave reads half of
+// a chunk's X fragments from LDS and dequantises half of each of its tiles,
+// and the two halves of a set run on different SIMDs.  The K-half-1 partial
+// sums are added to the K-half-0 ones through LDS at the end.
+template <int WT, int SDT, int MB, int TW, int NW, bool KS = false>
 __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
   using C = Tm<WT, MB, TW, NW>;
   constexpr int D = C::D;
   constexpr int LPT = C::LPT;
+  static_assert(!KS || (WT == W_INT4 && MB > 2 && NW % 2 == 0), "K halves: INT4 exact instances");
+  constexpr int NG = KS ? NW / 2 : NW;  // tile sets
   __shared__ typename C::Smem sm;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kg = KS ? (wave >> 1) : wave;  // tile set
+  const int kh = KS ? (wave & 1) : 0;      // K half
   const int lane = tid & 63, n = lane & 15, p4 = lane >> 4;
   const int NC = a.K >> 7;
   const int NT = a.N >> 4;
   const int g = blockIdx.x / a.splits, sp = blockIdx.x - g * a.splits;
   const int t0 = g * a.tpw;
   const int nt = (NT - t0) < a.tpw ? (NT - t0) : a.tpw;       // tiles of the group
-  const int ntw = nt > wave ? (nt - wave + NW - 1) / NW : 0;  // of this wave (uniform)
+  const int ntw = nt > kg ? (nt - kg + NG - 1) / NG : 0;      // of this wave (uniform)
   const int c0 = sp * a.cps;
   const int nk = (NC - c0) < a.cps ? (NC - c0) : a.cps;
   if (nt <= 0 || nk <= 0) return;
@@ -167,7 +180,7 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
   int tt[TW];
 #pragma unroll
   for (int i = 0; i < TW; ++i) {
-    const int j = wave + NW * i;
+    const int j = kg + NG * i;
     tt[i] = t0 + (j < nt ? j : 0);
   }
   // Weight byte offset of the lane's 16-byte load h of tile i at chunk 0.
@@ -178,8 +191,9 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
   for (int i = 0; i < TW; ++i)
 #pragma unroll
     for (int h = 0; h < LPT; ++h) {
-      const uint32_t inner =
-          WT == W_INT4 ? static_cast<uint32_t>(64 * n + 16 * p4) : static_cast<uint32_t>(128 * n + 64 * h + 16 * p4);
+      // (KS: the K half's 8 bytes, words 2kh and 2kh+1)
+      const uint32_t inner = WT == W_INT4 ? static_cast<uint32_t>(64 * n + 16 * p4 + 8 * kh)
+                                          : static_cast<uint32_t>(128 * n + 64 * h + 16 * p4);
       wo[i][h] = static_cast<uint32_t>(tt[i]) * static_cast<uint32_t>(NC) * C::TB + inner;
     }
   // Scale / zero-point source of lane 16i + n (tile i of the wave, row n) at chunk 0.
@@ -224,7 +238,8 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
     // INT4 round loads (scales, zero points) of a wave, issued with the
     // weights of the round's first chunk.
     constexpr int Lm = WT == W_INT4 && NTW > 0 ? (SDT == SCALE_F32 ? 3 : 2) : 0;
-    u32x4_t W[D][NTW > 0 ? NTW : 1][LPT];  // weight ring (registers)
+    using WV = std::conditional_t<KS, u32x2_t, u32x4_t>;
+    WV W[D][NTW > 0 ? NTW : 1][LPT];  // weight ring (registers)
 
     // X of round rho (chunks rho*R ..) into X buffer rho % 2; rounds past the
     // range read harmless in-range or out-of-range bytes that nothing uses.
@@ -262,7 +277,10 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < NTW; ++i)
 #pragma unroll
-          for (int h = 0; h < LPT; ++h) W[J][i][h] = C::wload(rs.w, wo[i][h], kw);
+          for (int h = 0; h < LPT; ++h) {
+            if constexpr (KS) W[J][i][h] = C::wload8(rs.w, wo[i][h], kw);
+            else W[J][i][h] = C::wload(rs.w, wo[i][h], kw);
+          }
       }
     };
 
@@ -291,12 +309,13 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
             zd[i] = 0u;
           }
         }
-        bf16x8_t A[MB][4];
+        constexpr int NST = KS ? 2 : 4;  // K16 steps of this wave per chunk
+        bf16x8_t A[MB][NST];
 #pragma unroll
         for (int b = 0; b < MB; ++b)
 #pragma unroll
-          for (int st = 0; st < 4; ++st) {
-            const int gseg = WT == W_INT4 ? 4 * p4 + st : 8 * (st >> 1) + 2 * p4 + (st & 1);
+          for (int st = 0; st < NST; ++st) {
+            const int gseg = WT == W_INT4 ? 4 * p4 + (KS ? 2 * kh : 0) + st : 8 * (st >> 1) + 2 * p4 + (st & 1);
             A[b][st] = __builtin_bit_cast(
                 bf16x8_t, *reinterpret_cast<const u32x4_t*>(xchunk + (16 * b + n) * 256 + ((gseg ^ n) * 16)));
           }
@@ -347,7 +366,7 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
               const float zp = static_cast<float>(1024u + z);
               const float cc = SDT == SCALE_F32 ? zp : -(zp * s);
 #pragma unroll
-              for (int st = 0; st < 4; ++st) {
+              for (int st = 0; st < NST; ++st) {
                 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
                 const uint32_t w = W[J][i][0][st];
                 float f[8];
@@ -451,12 +470,35 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
   else run(std::integral_constant<int, 0>{});
   // Drain the clamped prefetches before any exit.
   __builtin_amdgcn_s_waitcnt(0x0F70);
+  // K halves: half 1 hands its sums to half 0 of the same tile set, which
+  // adds them (half 0 + half 1, a fixed order) and stores the tiles.
+  int nto = ntw;  // tiles this wave stores
+  if constexpr (KS) {
+    __syncthreads();  // every wave is done with the X buffers
+    static_assert(NG * TW * MB * 64 * 16 <= 2 * C::XR, "K-half sums fit the X buffers");
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(&sm.xs[0][0]);
+    if (kh == 1) {
+#pragma unroll
+      for (int i = 0; i < TW; ++i)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) red[((kg * TW + i) * MB + b) * 64 + lane] = acc[i][b];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int i = 0; i < TW; ++i)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[i][b] += red[((kg * TW + i) * MB + b) * 64 + lane];
+    } else {
+      nto = 0;
+    }
+  }
 
   // Lane (n, p4), register e of block (i, b): row 16b + 4p4 + e, column 16 tt[i] + n.
   if (a.splits == 1) {
 #pragma unroll
     for (int i = 0; i < TW; ++i) {
-      if (i >= ntw) continue;
+      if (i >= nto) continue;
       const int col = 16 * tt[i] + n;
 #pragma unroll
       for (int b = 0; b < MB; ++b)
@@ -473,41 +515,49 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
     return static_cast<uint32_t>((static_cast<int64_t>(pp) * C::SLOT / 4 + ((wave * TW + i) * MB + b) * 64 + lane) *
                                  16);
   };
+  // Only the tiles this wave stores travel (uniform branches per wave).
 #pragma unroll
-  for (int i = 0; i < TW; ++i)
+  for (int i = 0; i < TW; ++i) {
+    if (i >= nto) continue;
 #pragma unroll
     for (int b = 0; b < MB; ++b) store_partial4(pr, poff(blockIdx.x, i, b), acc[i][b]);
+  }
   if (!arrive_last(a.counters, g, a.splits, &sm.flag)) return;
   f32x4_t sum[TW][MB];
 #pragma unroll
   for (int i = 0; i < TW; ++i)
 #pragma unroll
     for (int b = 0; b < MB; ++b) sum[i][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // Contributors in K-range order, up to four with all loads in flight
-  // (every load is a coherent round trip); a slot past the last contributor
-  // re-reads the last one and adds zero.
-  for (int q0 = 0; q0 < a.splits; q0 += 4) {
-    f32x4_t v[4][TW][MB];
+  // Contributors in K-range order, up to four (three-tile waves at 64 rows:
+  // two) with all loads in flight (every load is a coherent round trip); a
+  // slot past the last contributor re-reads the last one and adds zero.
+  constexpr int QF = TW * MB > 8 ? 2 : 4;
+  for (int q0 = 0; q0 < a.splits; q0 += QF) {
+    f32x4_t v[QF][TW][MB];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < QF; ++u) {
       const int q = q0 + u < a.splits ? q0 + u : a.splits - 1;
 #pragma unroll
-      for (int i = 0; i < TW; ++i)
+      for (int i = 0; i < TW; ++i) {
+        if (i >= nto) continue;
 #pragma unroll
         for (int b = 0; b < MB; ++b) v[u][i][b] = load_partial4(pr, poff(g * a.splits + q, i, b));
+      }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < QF; ++u) {
       const float keep = q0 + u < a.splits ? 1.0f : 0.0f;
 #pragma unroll
-      for (int i = 0; i < TW; ++i)
+      for (int i = 0; i < TW; ++i) {
+        if (i >= nto) continue;
 #pragma unroll
         for (int b = 0; b < MB; ++b) sum[i][b] += v[u][i][b] * keep;
+      }
     }
   }
 #pragma unroll
   for (int i = 0; i < TW; ++i) {
-    if (i >= ntw) continue;
+    if (i >= nto) continue;
     const int col = 16 * tt[i] + n;
 #pragma unroll
     for (int b = 0; b < MB; ++b)
@@ -532,8 +582,24 @@ bool tm_nw4() {
   return v;
 }
 
+// INT4 at 33..64 rows with one K range per tile group pairs the waves on the
+// K halves of their tiles (measured gate_up 34816x5120 M=64: 43.4 against
+// 45.3 us; with split K ranges, where the halves' partial sums travel too,
+// it was 3-10 % slower, so those keep one wave per tile).  HS_TM_KS=0 turns
+// it off.
+bool tm_ks() {
+  static const bool v = [] {
+    const char* e = std::getenv("HS_TM_KS");
+    return !(e != nullptr && e[0] == '0');
+  }();
+  return v;
+}
 int tm_mb(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
 int tm_nw(int wt, int M) { return M <= 32 || (wt == W_INT4 && !tm_nw4()) ? 8 : 4; }
+constexpr int kTmKsMaxTpw = 12;  // four tile sets of up to three tiles
+bool tm_use_ks(int wt, const GemmArgs& a) {
+  return wt == W_INT4 && a.M > 32 && tm_nw(wt, a.M) == 8 && tm_ks() && a.splits == 1 && a.tpw <= kTmKsMaxTpw;
+}
 int tm_tw(int wt, int M) { return tm_nw(wt, M) == 8 ? 2 : 3; }
 int tm_max_tpw(int wt, int M) { return tm_nw(wt, M) * tm_tw(wt, M); }
 int tm_slot_floats(int wt, int M) { return tm_nw(wt, M) * tm_tw(wt, M) * tm_mb(M) * 256; }
@@ -557,10 +623,11 @@ bool tiled_ok(const GemmArgs& a, int wt) {
   return tb < lim && xb < lim;
 }
 
-template <int WT, int SDT, int MB, int TW, int NW>
+template <int WT, int SDT, int MB, int TW, int NW, bool KS = false>
 static hipError_t launch_tiled_t(const GemmArgs& a, hipStream_t stream) {
   const int groups = (a.N / 16 + a.tpw - 1) / a.tpw;
-  hipLaunchKernelGGL((qgemm_tiled_kernel<WT, SDT, MB, TW, NW>), dim3(groups * a.splits), dim3(64 * NW), 0, stream, a);
+  hipLaunchKernelGGL((qgemm_tiled_kernel<WT, SDT, MB, TW, NW, KS>), dim3(groups * a.splits), dim3(64 * NW), 0, stream,
+                     a);
   return hipGetLastError();
 }
 
@@ -570,6 +637,7 @@ static hipError_t launch_tiled_s(const GemmArgs& a, hipStream_t stream) {
   if (mb == 1) return launch_tiled_t<WT, SDT, 1, 2, 8>(a, stream);
   if (mb == 2) return launch_tiled_t<WT, SDT, 2, 2, 8>(a, stream);
   if constexpr (WT == W_INT4) {
+    if (tm_use_ks(WT, a)) return launch_tiled_t<WT, SDT, 4, 3, 8, true>(a, stream);
     if (!tm_nw4()) return launch_tiled_t<WT, SDT, 4, 2, 8>(a, stream);
   }
   return launch_tiled_t<WT, SDT, 4, 3, 4>(a, stream);
