@@ -212,8 +212,10 @@ TmPlan tm_plan(int wt, int M, int N, int K) {
     const double mem = tpw * tb + 0.5 * mb * 4096.0;
     const double cmp = tw * comp;
     // a split group settles after its last K range: partial stores, the
-    // arrival, then coherent loads of four contributors per round trip
-    const double settle = S > 1 ? 30000.0 + 20000.0 * ((S + 3) / 4) : 0.0;
+    // arrival, then coherent loads of four contributors per round trip; the
+    // partials grow with the row blocks (measured at 64 rows: o_proj
+    // 8192->5120 19.2 us at 4 K ranges against 22.9 at 8)
+    const double settle = S > 1 ? (30000.0 + 20000.0 * ((S + 3) / 4)) * mb : 0.0;
     const double est = waves_per_cu * cps * (mem > cmp ? mem : cmp) + settle;
     if (est < best_est) {
       best_est = est;
