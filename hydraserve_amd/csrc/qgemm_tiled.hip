@@ -1,50 +1,52 @@
 // Decode-regime (1..64 activation rows) quantized weight GEMM over the
 // load-time tiled weight copy, for gfx950.
 //
-// INT4 tile words keep their K range (word j of a row's chunk: K 8j .. 8j+7)
-// with the nibbles paired for the MFMA operand: nibble i (i < 4) holds
-// K 8j + 2i and nibble i + 4 holds K 8j + 2i + 1, so ((w >> 4i) & 0x000F000F)
-// puts two consecutive-K weights in the two halves of a dword
-// (hydraserve_amd/kernels/tiles.py makes the copy).
-//
 // Replaces the Triton launches of hydraserve/kernels/awq.py:52-74
 // (_awq_gemm_kernel, awq.py:82-142) and hydraserve/kernels/fp8.py:68-96
-// (_fp8_gemm_kernel, fp8.py:104-168) when the weight carries a tiled copy:
-// tile (t, c) = rows 16t..16t+15 of the 128-wide K chunk c, stored
-// contiguously (INT4: 16 rows x 64 bytes = 1 KiB; FP8: 16 rows x 128 bytes =
-// 2 KiB) at byte (t * K/128 + c) * tile_bytes.  Every weight load instruction
-// therefore reads one contiguous KiB, the access HBM serves best, where the
-// row-major checkpoint layout gives 16-32 pieces of 32-64 bytes on distinct
-// DRAM pages.
+// (_fp8_gemm_kernel, fp8.py:104-168) when the weight carries a tiled copy
+// (hydraserve_amd/kernels/tiles.py): tile (t, c) = rows 16t..16t+15 of the
+// 128-wide K chunk c, stored contiguously (INT4: 16 rows x 64 bytes = 1 KiB;
+// FP8: 16 rows x 128 bytes = 2 KiB) at byte (c * N/16 + t) * tile_bytes, i.e.
+// chunk-major: the tiles of one K chunk are adjacent, so the whole grid,
+// walking K in step, reads one window of the weight at a time.  Every weight
+// load instruction reads one contiguous KiB.  INT4 tile words keep their K
+// range (word j of a row's chunk: K 8j .. 8j+7) with the nibbles paired for
+// the MFMA operand: nibble i (i < 4) holds K 8j + 2i and nibble i + 4 holds
+// K 8j + 2i + 1, so ((w >> 4i) & 0x000F000F) puts two consecutive-K weights
+// in the two halves of a dword.
 //
 // Work split.  The N/16 tiles are cut into groups of `tpw` consecutive tiles
 // and K into `splits` ranges of `cps` chunks; workgroup p takes tile group
-// p / splits over K range p % splits.  Its four wavefronts own the group's
-// tiles round-robin (wave w: local tiles w, w+4, w+8) and walk the K range
-// together, one chunk per step:
-//   * the chunk's X tile [16*MB rows x 128] (shared by the four waves), each
-//     wave's weight tiles, and their scales / zero-point words go global ->
-//     LDS by LDS-DMA into a ring of D chunk slots, D-1 chunks ahead;
-//   * per step every wave waits for its own loads of the chunk, one barrier
-//     makes the other waves' X loads visible, and the slot of the previous
-//     chunk (which every wave has finished reading) takes the next loads;
-//   * weights are dequantised in registers to the reference's values,
-//     INT4 bf16_rne((q - z) * s) (awq.py:18-22, 136-137) via v_fma_mix on the
-//     fp16 1024+q, FP8 e4m3 -> bf16 exactly with the block scale applied to
-//     the chunk's fp32 MFMA result, and feed v_mfma_f32_16x16x32_bf16:
-//     lane (n, p) = (lane % 16, lane / 16) supplies weight row n and X row n of
-//     each 16-row block, K offsets 32p + 8s .. +8 at step s.
+// p / splits over K range p % splits.  Its waves own the group's tiles
+// round-robin and walk the K range together, one chunk per step:
+//   * each wave's weights go global -> registers through a ring of D chunks
+//     unrolled by its depth (D-1 chunks in flight); the chunk's X rows go
+//     global -> LDS by LDS-DMA in double-buffered rounds of R chunks with one
+//     workgroup barrier per round; FP8 scales go by LDS-DMA per chunk, INT4
+//     scales and zero points by one 16-byte LDS-DMA load per lane per round
+//     of 8 chunks;
+//   * weights are dequantised in registers and feed v_mfma_f32_16x16x32_bf16:
+//     lane (n, p) = (lane % 16, lane / 16) supplies weight row n and X row n
+//     of each 16-row block, K offsets 32p + 8s .. +8 at step s.  INT4 up to
+//     32 rows: the group rewrite (128 + q as bf16, X sums from an all-ones
+//     MFMA, acc += s (T - (128+z) Xg)); above, the reference's values
+//     bf16_rne((q - z) * s) (awq.py:18-22, 136-137) via v_fma_mix on fp16
+//     1024+q.  FP8: e4m3 -> bf16 exactly, the block scale applied to the
+//     chunk's fp32 MFMA result;
+//   * the loop body has no branches (skipped ring steps run after the loop,
+//     each wave's code is specialised on its tile count, X loads past M are
+//     out-of-range buffer loads), so the waits on loads in flight are exact.
 // With one K range the workgroup stores bf16 Y directly.  With several, each
 // workgroup writes an fp32 partial of its tile group, and the last of the
 // group's workgroups to arrive sums the partials in K-range order
 // (deterministic) and stores Y.
 //
-// LDS slot layout (bytes): X rows r = 0 .. 16*MB-1 at 256r, the 16-byte
-// K segment g at ((g ^ (r & 15)) * 16); per wave its TW weight tiles (INT4:
-// 16-byte part p of row n at 64n + 16((p + n/4) & 3); FP8: part q of row n at
-// 128n + 16((q + n/2) & 7)), so the reads of 8 consecutive lanes hit distinct
-// banks; per wave 64 scale dwords and (INT4) 64 zero-point dwords, lane
-// 16i + n holding tile i's row n.
+// LDS layout: X rows r = 0 .. 16*MB-1 of a chunk at 256r, the 16-byte K
+// segment g at ((g ^ (r & 15)) * 16), so 16 consecutive rows' fragment reads
+// hit distinct banks; per wave and 8-chunk round the INT4 scales (lane
+// 16i + n: tile i's row n, 16 bytes per half of 4 chunks for fp32 scales)
+// and zero-point words (lane 4i + 2h + half: tile i's word row h, chunks
+// 4 half .. +3).
 #include <cstdlib>
 #include <type_traits>
 
@@ -194,7 +196,7 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
       // (KS: the K half's 8 bytes, words 2kh and 2kh+1)
       const uint32_t inner = WT == W_INT4 ? static_cast<uint32_t>(64 * n + 16 * p4 + 8 * kh)
                                           : static_cast<uint32_t>(128 * n + 64 * h + 16 * p4);
-      wo[i][h] = static_cast<uint32_t>(tt[i]) * static_cast<uint32_t>(NC) * C::TB + inner;
+      wo[i][h] = static_cast<uint32_t>(tt[i]) * C::TB + inner;
     }
   // Scale / zero-point source of lane 16i + n (tile i of the wave, row n) at chunk 0.
   const int li = (lane >> 4) < TW ? (lane >> 4) : TW - 1;
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
           const uint32_t sb = static_cast<uint32_t>((se0 + c) * ses) & ~3u;
           C::dma(rs.s, &sm.ring[J][0] + wave * 256, 4, sb, 0);
         }
-        const uint32_t kw = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c) * C::TB);
+        const uint32_t kw = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c) * static_cast<uint32_t>(NT) * C::TB);
 #pragma unroll
         for (int i = 0; i < NTW; ++i)
 #pragma unroll

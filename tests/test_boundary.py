@@ -259,10 +259,11 @@ def test_tiled_copies_round_trip_and_are_dropped_by_fuse_split():
     assert isinstance(t, TiledInt4Weight) and isinstance(t, PackedInt4Weight)
     assert t.tiles.shape == (3, 3, 16, 16)
     assert torch.equal(untile_int4(t.tiles, n, k), w.packed)
-    # tile (1, 2) = rows 16..31, words 32..47, nibbles paired: K offset i of a
-    # word sits at nibble i/2 (even i) or 4 + i/2 (odd i)
+    # tiles are chunk-major: tiles[c, t] = rows 16t..16t+15 of chunk c.
+    # Tile (t=1, c=2) = rows 16..31, words 32..47, nibbles paired: K offset i
+    # of a word sits at nibble i/2 (even i) or 4 + i/2 (odd i)
     src = w.packed[16:32, 32:48].to(torch.int64) & 0xFFFFFFFF
-    dst = t.tiles[1, 2].to(torch.int64) & 0xFFFFFFFF
+    dst = t.tiles[2, 1].to(torch.int64) & 0xFFFFFFFF
     for i in range(8):
         pos = i // 2 if i % 2 == 0 else 4 + i // 2
         assert torch.equal((src >> (4 * i)) & 15, (dst >> (4 * pos)) & 15)
@@ -272,6 +273,7 @@ def test_tiled_copies_round_trip_and_are_dropped_by_fuse_split():
     )
     tf = tile_fp8_weight(f)
     assert torch.equal(tf.tiles[1, 1], f.data.view(torch.uint8)[16:32, 128:256])
+    assert torch.equal(tf.tiles[0, 1], f.data.view(torch.uint8)[16:32, 0:128])
     parts = hs.split_linear_weight(t, (16, 32))
     assert all(type(p) is PackedInt4Weight for p in parts)
     fused = hs.concatenate_linear_weights([t, t])
