@@ -98,8 +98,8 @@ PMC_TRAFFIC_KIB = {
     ("int4", "gate_up", 64, "row-major"): (69799.2, 28954.0),
     ("int4", "down", 64, "row-major"): (36461.5, 9866.2),
     ("int4", "down", 16, "row-major"): (26201.5, 1452.5),
-    ("int4", "gate_up", 64, "tiled"): (48972.6, 4352.02),
-    ("int4", "gate_up", 1, "tiled"): (45994.0, 68.0),
+    ("int4", "gate_up", 64, "tiled"): (49033.0, 4352.0),
+    ("int4", "gate_up", 1, "tiled"): (46148.8, 68.0),
 }
 FETCH_CAL, WRITE_CAL = 2.0, 1.0
 
