@@ -13,7 +13,10 @@ unpack wants); on MI355X a streaming probe of the gate_up weight went from
 ~3.6 to ~5.3 TB/s with this layout.  Tiles are stored chunk-major (all N/16
 tiles of chunk 0, then chunk 1, ...): the kernel's workgroups walk K in step,
 so the grid reads one window of the weight at a time (FP8 gate_up M=1:
-35.9 -> 33.0 us against the tile-major order, INT4 1-3 % faster).  The copy is made once, at load time, and
+35.9 -> 33.0 us against the tile-major order, INT4 1-3 % faster).  Inside
+an FP8 tile the bytes are ordered so that each of a lane's two 16-byte loads
+is one contiguous KiB across the wave (two halves of 64 K each; the 16 bytes
+of row r at K quarter p of a half at (16p + r) * 16).  The copy is made once, at load time, and
 the row-major tensors stay in the weight (every other kernel reads them, and
 the tiled kernel only takes activations of at most 64 rows); the values are
 not changed (tests check the round trip and the GEMM results).
@@ -37,7 +40,7 @@ class TiledInt4Weight(PackedInt4Weight):
 
 @dataclass(frozen=True, slots=True)
 class TiledFP8Weight(BlockScaledFP8Weight):
-    tiles: Any = None  # uint8 [K/128, N/16, 16, 128]
+    tiles: Any = None  # uint8 [K/128, N/16, 2, 4, 16, 16]: [chunk, tile, K half, K quarter, row, byte]
 
 
 def _pair_nibbles(words, inverse: bool = False):
@@ -77,5 +80,8 @@ def tile_fp8_weight(weight: BlockScaledFP8Weight) -> TiledFP8Weight:
     if n % 16 or k % 128:
         raise ValueError("FP8 tiles need N % 16 == 0 and K % 128 == 0")
     d = weight.data.view(torch.uint8)[:n, :k]
-    tiles = d.reshape(n // 16, 16, k // 128, 128).permute(2, 0, 1, 3).contiguous()
+    # tile bytes [h][p][r][16]: row r's bytes 64h + 16p .. +16 (the tiled
+    # kernel's lane 16p + r reads them with its load h, one contiguous KiB
+    # per load instruction)
+    tiles = d.reshape(n // 16, 16, k // 128, 2, 4, 16).permute(2, 0, 3, 4, 1, 5).contiguous()
     return TiledFP8Weight(weight.data, weight.scale_inv, weight.original_shape, weight.block_size, tiles)

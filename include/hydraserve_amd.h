@@ -127,10 +127,11 @@ int hs_fp8_gemm(const void* x, int64_t ldx,
  * (the "kernel-native layout" of the weight; same GPU branch of awq_linear /
  * fp8_linear, hydraserve/kernels/awq.py:25-75, hydraserve/kernels/fp8.py:24-97).
  * tiles: rows 16t..16t+15 of 128-wide K chunk c stored contiguously as tile
- * (t, c) at byte (c * N/16 + t) * TB, TB = 1024 (INT4: 16 rows x 16 int32
- * words, nibbles paired as kernels/tiles.py describes) or 2048 (FP8: 16 rows
- * x 128 bytes), each tile's rows in order: i.e.
- * packed.view(N/16, 16, K/128, TB/16).permute(2, 0, 1, 3).
+ * (t, c) at byte (c * N/16 + t) * TB.  INT4: TB = 1024, 16 rows x 16 int32
+ * words, rows in order, nibbles paired as kernels/tiles.py describes
+ * (packed.view(N/16, 16, K/128, 16).permute(2, 0, 1, 3)).  FP8: TB = 2048,
+ * the 16 bytes of row r at K 64h + 16p .. +16 at byte 1024h + 16(16p + r)
+ * of the tile (data.view(N/16, 16, K/128, 2, 4, 16).permute(2, 0, 3, 4, 1, 5)).
  * Requires N % 16 == 0 and K % 128 == 0 for the tiles to be read; the
  * row-major weight is still passed and used by the kernels that do not read
  * tiles (the tiles serve the block-major decode kernel at 1..16 rows, where

@@ -272,8 +272,12 @@ def test_tiled_copies_round_trip_and_are_dropped_by_fuse_split():
         torch.ones(1, 2), (32, 256),
     )
     tf = tile_fp8_weight(f)
-    assert torch.equal(tf.tiles[1, 1], f.data.view(torch.uint8)[16:32, 128:256])
-    assert torch.equal(tf.tiles[0, 1], f.data.view(torch.uint8)[16:32, 0:128])
+    # FP8 tile (t=1, c=1): rows 16..31, K 128..255; byte j of row r at K
+    # 64h + 16p + j sits at tiles[c, t, h, p, r, j]
+    src8 = f.data.view(torch.uint8)[16:32, 128:256].reshape(16, 2, 4, 16)
+    assert torch.equal(tf.tiles[1, 1], src8.permute(1, 2, 0, 3))
+    src8 = f.data.view(torch.uint8)[16:32, 0:128].reshape(16, 2, 4, 16)
+    assert torch.equal(tf.tiles[0, 1], src8.permute(1, 2, 0, 3))
     parts = hs.split_linear_weight(t, (16, 32))
     assert all(type(p) is PackedInt4Weight for p in parts)
     fused = hs.concatenate_linear_weights([t, t])
