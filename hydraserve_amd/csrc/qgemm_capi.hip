@@ -192,7 +192,11 @@ TmPlan tm_plan(int wt, int M, int N, int K) {
   const int64_t NT = N / 16, NC = K / 128;
   const int mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   const double tb = wt == W_INT4 ? 1024.0 : 2048.0;
-  const double comp = wt == W_INT4 ? 2600.0 : 1000.0 + 250.0 * mb;
+  // per-SIMD compute of one tile and chunk, in the units of the memory term:
+  // INT4 at 33..64 rows dequantises exactly and runs four MFMA row blocks
+  // (measured at 64 rows: down 17408->5120 31.8 us at 6 K ranges of 8-tile
+  // groups against 33.7 at 8 of 10-tile groups, whose busiest SIMD holds 3)
+  const double comp = wt == W_INT4 ? (mb >= 4 ? 8000.0 : 2600.0) : 1000.0 + 250.0 * mb;
   double best_est = 1e30;
   const int cand[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
   for (int s0 : cand) {
