@@ -27,6 +27,10 @@ CASES = (
     + [("int4", m, 2048, 2048, sdt) for m in (8, 64) for sdt in (torch.float16, torch.float32)]
     + [("fp8", m, 4096, 2048, sdt) for m in (1, 16, 33, 64) for sdt in (torch.float32, torch.bfloat16)]
     + [("fp8", m, 272, 1024, torch.float16) for m in (3, 40)]
+    # 10 K chunks, 65 tiles: K ranges that end inside a ring round and an
+    # 8-chunk scale round, a ragged last tile group
+    + [("int4", m, 1040, 1280, torch.bfloat16) for m in (1, 16, 40)]
+    + [("fp8", m, 1040, 1280, torch.bfloat16) for m in (1, 40)]
     # 129..192 rows: 128 rows row-major, the rest through the tiled kernel
     + [("int4", 160, 4096, 1024, torch.bfloat16), ("fp8", 192, 4096, 2048, torch.float32),
        ("int4", 190, 1024, 4096, torch.float16)]
