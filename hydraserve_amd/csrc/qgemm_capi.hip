@@ -363,7 +363,7 @@ Plan make_plan(int wt, int M, int N, int K, bool kfull, bool fast, bool wide, bo
     p.wide = true;
     p.TM = static_cast<int>(cdiv(M, 256));
     p.T = p.TM * static_cast<int>(cdiv(N, 256));
-    p.G = K / 64;
+    p.G = K / 128;  // stream-K unit: one 128-K group
     p.U = static_cast<int64_t>(p.T) * p.G;
     p.P = static_cast<int>(p.U < cus ? p.U : cus);
     p.slot_floats = wide_slot_floats();

@@ -132,14 +132,29 @@ struct Wide {
   };
 
   static __device__ __forceinline__ void load_raw(const Rsrc& rs, const Offs& o, Raw& r, int c) {
-    const uint32_t g = static_cast<uint32_t>(c >> 1);
-    constexpr uint32_t SES = SDT == SCALE_F32 ? 4 : 2;
-    const uint32_t soff_s = __builtin_amdgcn_readfirstlane(g * SES);
-    const uint32_t soff_z = __builtin_amdgcn_readfirstlane(g * 4u);
+    load_w(rs, o, r, c);
+    load_sz(rs, o, r, c);
+  }
+
+  // Weights of unit c into r.
+  static __device__ __forceinline__ void load_w(const Rsrc& rs, const Offs& o, Raw& r, int c) {
     const uint32_t soff_w = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c) * (WT == W_INT4 ? 32u : 64u));
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       u32x4_t* dst = j == 0 ? r.q0 : r.q1;
+      dst[0] = bload<u32x4_t>(rs.w, o.w[j], soff_w);
+      if constexpr (WT == W_FP8) dst[1] = bload<u32x4_t>(rs.w, o.w[j] + 16u, soff_w);
+    }
+  }
+
+  // Scale bits and (INT4) zero-point words of unit c's group into r.
+  static __device__ __forceinline__ void load_sz(const Rsrc& rs, const Offs& o, Raw& r, int c) {
+    const uint32_t g = static_cast<uint32_t>(c >> 1);
+    constexpr uint32_t SES = SDT == SCALE_F32 ? 4 : 2;
+    const uint32_t soff_s = __builtin_amdgcn_readfirstlane(g * SES);
+    const uint32_t soff_z = __builtin_amdgcn_readfirstlane(g * 4u);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
       uint32_t sb;
       if constexpr (SDT == SCALE_F32) {
         sb = bload<uint32_t>(rs.s, o.s[j], soff_s);
@@ -147,12 +162,7 @@ struct Wide {
         sb = bload<uint16_t>(rs.s, o.s[j], soff_s);
       }
       uint32_t zw = 0;
-      dst[0] = bload<u32x4_t>(rs.w, o.w[j], soff_w);
-      if constexpr (WT == W_INT4) {
-        zw = bload<uint32_t>(rs.z, o.z[j], soff_z);
-      } else {
-        dst[1] = bload<u32x4_t>(rs.w, o.w[j] + 16u, soff_w);
-      }
+      if constexpr (WT == W_INT4) zw = bload<uint32_t>(rs.z, o.z[j], soff_z);
       if (j == 0) {
         r.s0 = sb;
         r.z0 = zw;
@@ -238,7 +248,10 @@ struct Wide {
   // (the next unit's X and weights, issued one unit ago) and the workgroup
   // barrier; then the loads of the unit after next are issued: X by LDS-DMA
   // into bd (last read before this barrier) and its weights into Rc (last
-  // decoded during step 2).
+  // decoded during step 2).  SHARE: unit cnext2 is the odd half of the
+  // 128-K group whose even half Rn holds (landed at that wait), so its scale
+  // and zero point are copied from Rn instead of loaded again.
+  template <bool SHARE>
   static __device__ __forceinline__ void unit(Smem& sm, int bc, int bn, int bd, int cnext2, bf16x8_t (&A)[MI],
                                               bf16x8_t (&B)[2], Raw& Rc, const Raw& Rn, const Rsrc& rs,
                                               const Offs& o, const uint32_t (&aoff)[4], f32x16_t (&acc)[MI][2],
@@ -249,7 +262,15 @@ struct Wide {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
         dma_x(rs, o, sm, bd, cnext2, wave);
-        load_raw(rs, o, Rc, cnext2);
+        load_w(rs, o, Rc, cnext2);
+        if constexpr (SHARE) {
+          Rc.s0 = Rn.s0;
+          Rc.s1 = Rn.s1;
+          Rc.z0 = Rn.z0;
+          Rc.z1 = Rn.z1;
+        } else {
+          load_sz(rs, o, Rc, cnext2);
+        }
       }
       bf16x8_t An[MI], Bn[2];
 #pragma unroll
@@ -400,8 +421,9 @@ struct Wide {
   }
 };
 
-// a.G = 64-wide K units per tile, a.T = tiles, a.TM = tiles along M,
-// a.U = T * G, a.P = workgroups.  Tile t covers rows (t / (T/TM)) * 256 and
+// a.G = 128-wide K groups per tile (the stream-K unit; the pipeline runs on
+// 64-wide halves of them), a.T = tiles, a.TM = tiles along M, a.U = T * G,
+// a.P = workgroups.  Tile t covers rows (t / (T/TM)) * 256 and
 // weight rows (t % (T/TM)) * 256.
 template <int WT, int SDT, bool SILU>
 __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
@@ -436,10 +458,11 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
   int64_t u = u0;
   while (u < u1) {
     const int t = static_cast<int>(u / a.G);
-    const int cb = static_cast<int>(u - static_cast<int64_t>(t) * a.G);
-    const int ce = static_cast<int>((u1 - static_cast<int64_t>(t) * a.G) < a.G ? (u1 - static_cast<int64_t>(t) * a.G)
+    const int gb = static_cast<int>(u - static_cast<int64_t>(t) * a.G);
+    const int ge = static_cast<int>((u1 - static_cast<int64_t>(t) * a.G) < a.G ? (u1 - static_cast<int64_t>(t) * a.G)
                                                                                 : a.G);
-    const int n = ce - cb;
+    // 64-wide units [cb, ce): an even start and an even count.
+    const int cb = 2 * gb, ce = 2 * ge, n = ce - cb;
     int tm, tn;
     W::coords(a, t, tm, tn);
 
@@ -448,7 +471,7 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
     typename W::Offs o;
     W::offsets(a, o, tm, tn, wave, l32, h, tid);
     typename W::Raw r0, r1;
-    const int c1 = cb + 1 < ce ? cb + 1 : ce - 1;
+    const int c1 = cb + 1;
     W::dma_x(rs, o, sm, 0, cb, wave);
     W::dma_x(rs, o, sm, W::XB, c1, wave);
     W::load_raw(rs, o, r0, cb);
@@ -467,30 +490,17 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
 
     // LDS buffers rotate b0 (this unit) -> b1 (next) -> b2 (DMA target).
     // Unit indices past the tile's last are clamped (their loads are
-    // harmless and never used).  Units run in pairs so that the two
-    // raw-weight register sets alternate without copies, and the pair loop
-    // has a single exit (a break between the two units makes the register
-    // allocator shuffle the accumulators); an odd unit count peels one unit
-    // first and swaps the sets once.
+    // harmless and never used).  Units run in pairs (one 128-K group) so
+    // that the two raw-weight register sets alternate without copies and
+    // the odd half reuses the even half's scale and zero point; the pair
+    // loop has a single exit (a break between the two units makes the
+    // register allocator shuffle the accumulators).
     int b0 = 0, b1 = W::XB, b2 = 2 * W::XB;
-    int q = 0;
-    if (n & 1) {
-      const int cn = cb + 2 < ce ? cb + 2 : ce - 1;
-      W::unit(sm, b0, b1, b2, cn, A, B, r0, r1, rs, o, aoff, acc, wave, nm, mg);
-      const int tb = b0;
-      b0 = b1;
-      b1 = b2;
-      b2 = tb;
-      const typename W::Raw tr = r0;
-      r0 = r1;
-      r1 = tr;
-      q = 1;
-    }
-    for (; q < n; q += 2) {
+    for (int q = 0; q < n; q += 2) {
       const int cn0 = cb + q + 2 < ce ? cb + q + 2 : ce - 1;
       const int cn1 = cb + q + 3 < ce ? cb + q + 3 : ce - 1;
-      W::unit(sm, b0, b1, b2, cn0, A, B, r0, r1, rs, o, aoff, acc, wave, nm, mg);
-      W::unit(sm, b1, b2, b0, cn1, A, B, r1, r0, rs, o, aoff, acc, wave, nm, mg);
+      W::template unit<false>(sm, b0, b1, b2, cn0, A, B, r0, r1, rs, o, aoff, acc, wave, nm, mg);
+      W::template unit<true>(sm, b1, b2, b0, cn1, A, B, r1, r0, rs, o, aoff, acc, wave, nm, mg);
       const int tb = b0;
       b0 = b2;
       b2 = b1;
@@ -501,7 +511,7 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
     __syncthreads();
     W::finish_tile(a, sm, acc, t, tm, tn, v, u0, u1, tid);
     __syncthreads();
-    u += n;
+    u += ge - gb;
   }
 }
 
