@@ -8,7 +8,7 @@ one pass over those 8 GEMMs through the product entry point
 (hydraserve_amd.awq_linear -> C ABI -> HIP), on weights as the loader leaves
 them (`--layout tiled`, the default: the checkpoint's packed tensors plus the
 load-time tiled copy that load_linear_weights(tile=True) adds, read by the
-tiled decode kernel up to 64 rows; `--layout row-major`: the checkpoint tensors
+tiled decode kernel up to 64 rows and by the 256x256 prefill kernel above; `--layout row-major`: the checkpoint tensors
 alone).  `value_row_major` is the same step on the checkpoint tensors alone.  Inputs are synthetic and
 resident in HBM before timing; weights rotate over several independent copies
 (> 256 MB MALL) so every GEMM streams its weights from HBM.  W eager warmup
@@ -287,8 +287,8 @@ def tiled(kind, ws):
 def measure_all(torch, gen, dev, headline, layout):
     """One timed entry per (config, shape, M, layout): graphs of back-to-back
     launches over rotated weight copies, HIP events around the replays.
-    Decode rows (M <= 64) are timed on both weight layouts, prefill rows on the
-    checkpoint tensors (the prefill kernels read those in either layout).
+    Every row is timed on both weight layouts (the tiled decode kernel reads
+    the tiled copy up to 64 rows, the 256x256 prefill kernel above that).
     `headline`: the config-1 entries already measured."""
     out = []
     for cfg, kind, name, m_list in ALL_CONFIGS:
@@ -297,12 +297,10 @@ def measure_all(torch, gen, dev, headline, layout):
         per_copy = int4_bytes(n, k) if kind == "int4" else fp8_bytes(n, k)
         copies = copies_for(per_copy)
         ws = make(torch, n, k, copies, gen, dev)
-        wt = tiled(kind, ws) if min(m_list) <= 64 else None
+        wt = tiled(kind, ws)
         for m in m_list:
             x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
             for lay, wl in (("row-major", ws), ("tiled", wt)):
-                if lay == "tiled" and m > 64:
-                    continue
                 c = Case(kind, name, n, k, m, wl, x)
                 reps = 10 if m <= 64 else 4
                 ms, _ = graph_time_ms(torch, c.call, reps, 2 * copies)
@@ -313,11 +311,11 @@ def measure_all(torch, gen, dev, headline, layout):
                 print(json.dumps(r), file=sys.stderr, flush=True)
         del ws, wt
         torch.cuda.empty_cache()
-    # config 4: summed latency of one decoder layer's projections (decode rows
-    # on the --layout weights, prefill rows on the checkpoint tensors)
+    # config 4: summed latency of one decoder layer's projections on the
+    # --layout weights
     layer = {}
     for r in headline + out:
-        if r["M"] <= 64 and r.get("layout", layout) != layout:
+        if r.get("layout", layout) != layout:
             continue
         if r["kind"] == "int4" and r["shape"] in ("qkv", "o_proj", "gdn_in", "gate_up", "down") and r["M"] in (64, 1024):
             layer.setdefault(r["M"], []).append(r["us"])
@@ -524,7 +522,7 @@ def main():
         entries, c4 = measure_all(torch, gen, dev, result["per_shape"], args.layout)
         result["per_shape"] += entries
         result["config4_layer"] = c4
-        prefill = [r for r in entries if r["bound"] == "mfma"]
+        prefill = [r for r in entries if r["bound"] == "mfma" and r["layout"] == args.layout]
         dom_p = max(prefill, key=lambda r: r["us"])
         result["roofline_prefill"] = {
             "bound": "mfma",
@@ -533,7 +531,8 @@ def main():
             "unit": "TFLOP/s",
             "frac": dom_p["roofline_frac"],
             "traffic": None,
-            "kernel": f"{dom_p['kind'].upper()} prefill {dom_p['shape']} M={dom_p['M']} ({dom_p['N']}x{dom_p['K']})",
+            "kernel": f"{dom_p['kind'].upper()} prefill {dom_p['shape']} M={dom_p['M']} ({dom_p['N']}x{dom_p['K']}), "
+            f"{args.layout} weights",
             "flops_per_launch": 2 * dom_p["M"] * dom_p["N"] * dom_p["K"],
             "us_per_launch": dom_p["us"],
         }

@@ -28,6 +28,7 @@ int mid_slot_floats(int bmi, int nj, int nw);
 bool mid_ok(const GemmArgs& a, int wt);
 int wide_slot_floats();
 bool wide_ok(const GemmArgs& a, int wt);
+bool wide_tiles_ok(const GemmArgs& a, int wt);
 bool rows_ok(const GemmArgs& a, int wt, int P, int* nblk_out, bool* xl_out, int* ms_out, int xl_pref);
 hipError_t launch_rows(int wt, const GemmArgs& a, int nblk, bool xl, int ms, hipStream_t stream);
 extern int rows_kw8;
@@ -76,6 +77,7 @@ struct Tuning {
   int prefill_bm = 0;
   int wide_off = 0;         // 1: never use the 256x256-tile prefill kernel
   int wide_min_m = 0;      // smallest M for it (0 = 129)
+  int wide_tiles_off = 0;  // 1: it reads the row-major weight even when a tiled copy is given
   int tune = 0;            // GemmArgs::tune experiment bits
   int mid_off = 0;         // 1: never use the LDS-DMA streaming kernel for 17..64 rows
   int mid_min_m = 0;       // smallest M for it (0 = 17)
@@ -120,6 +122,7 @@ const Tuning& tuning() {
     r.prefill_bm = env_int("HS_PREFILL_BM");
     r.wide_off = env_int("HS_WIDE_OFF");
     r.wide_min_m = env_int("HS_WIDE_MIN_M");
+    r.wide_tiles_off = env_int("HS_WIDE_TILES_OFF");
     r.tune = env_int("HS_TUNE");
     r.mid_off = env_int("HS_MID_OFF");
     r.mid_min_m = env_int("HS_MID_MIN_M");
@@ -457,7 +460,9 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   // partition per workgroup, no workspace.  Block-major when X fits in LDS.
   // The register-streamed kernel wins on narrow outputs (N < K) from 5
   // (INT4) / 9 (FP8) activation rows; the row-partitioned kernels below keep
-  // fewer rows and the wide outputs.
+  // fewer rows and the wide outputs.  Of the kernels below only the 256x256
+  // prefill kernel reads tiles.
+  const void* const tiles = a.wtiles;
   a.wtiles = nullptr;
   const bool skinny_auto = a.N < a.K && a.M >= (wt == W_INT4 ? 5 : 9);
   const bool use_skinny = tn.skinny != 2 && (tn.skinny == 1 || skinny_auto) && a.M <= 64 &&
@@ -505,6 +510,10 @@ int run_gemm(int wt, GemmArgs& a, void* workspace, int64_t workspace_bytes, hipS
   a.P = p.P;
   a.counters = reinterpret_cast<int*>(workspace);
   a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.counter_bytes);
+  if (p.wide && !tn.wide_tiles_off) {
+    a.wtiles = tiles;
+    if (!wide_tiles_ok(a, wt)) a.wtiles = nullptr;
+  }
   hipError_t e = p.skinny   ? launch_skinny(wt, a, p.SS, p.SNB, p.SKC, skinny_xd(a.M), stream)
                  : p.mid    ? launch_mid(wt, a, p.BMI, p.NJ, p.NW, stream)
                  : p.stream ? launch_stream(wt, a, p.MT, p.S, stream)

@@ -39,6 +39,13 @@
 // of every MFMA step t takes K offsets 32h + 8t .. +8, so each lane reads one
 // contiguous 16-byte (INT4) / 32-byte (FP8) run of its weight row per unit.
 //
+// Tiled weights (TL, the load-time tiled copy: rows 16t..16t+15 of 128-wide
+// K chunk g at byte (g * N/16 + t) * TB, TB = 1 KiB INT4 / 2 KiB FP8): the
+// same registers come from fewer cache lines per load instruction (FP8: four
+// contiguous 256-byte runs instead of 32 rows x 32 bytes; INT4: 16 rows x
+// 64 bytes per two tiles instead of 32 lines), and INT4 words arrive with
+// their nibbles paired (position i < 4 holds K offset 2i, i + 4 holds 2i + 1).
+//
 // Shapes (checked on the host, wide_ok): K a multiple of 128, X and W rows
 // 16-byte aligned; M and N are free (rows past the end are clamped on load
 // and masked on store).
@@ -50,7 +57,7 @@ namespace hsq {
 
 constexpr int WD_THREADS = 256;
 
-template <int WT, int SDT, bool SILU = false>
+template <int WT, int SDT, bool SILU = false, bool TL = false>
 struct Wide {
   static constexpr int BM = 256;
   static constexpr int BN = 256;
@@ -124,6 +131,10 @@ struct Wide {
         o.s[j] = static_cast<uint32_t>((row >> 7) * a.lds * SES);
         o.z[j] = o.zsh[j] = 0;
       }
+      if constexpr (TL) {
+        if constexpr (WT == W_INT4) o.w[j] = static_cast<uint32_t>((row >> 4) * 1024 + (row & 15) * 64 + 16 * h);
+        else o.w[j] = static_cast<uint32_t>((row >> 4) * 2048 + 16 * (32 * h + (row & 15)));
+      }
     }
   }
 
@@ -131,19 +142,29 @@ struct Wide {
     __amdgpu_buffer_rsrc_t x, w, s, z;
   };
 
-  static __device__ __forceinline__ void load_raw(const Rsrc& rs, const Offs& o, Raw& r, int c) {
-    load_w(rs, o, r, c);
+  static __device__ __forceinline__ void load_raw(const Rsrc& rs, const Offs& o, Raw& r, int c, uint32_t ts) {
+    load_w(rs, o, r, c, ts);
     load_sz(rs, o, r, c);
   }
 
-  // Weights of unit c into r.
-  static __device__ __forceinline__ void load_w(const Rsrc& rs, const Offs& o, Raw& r, int c) {
-    const uint32_t soff_w = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c) * (WT == W_INT4 ? 32u : 64u));
+  // Weights of unit c into r.  Tiled: chunk c/2 starts at byte
+  // (c/2) * tstride, and unit c is its half c % 2 (INT4: bytes 32.. of each
+  // 64-byte tile row; FP8: the second KiB of each tile).
+  static __device__ __forceinline__ void load_w(const Rsrc& rs, const Offs& o, Raw& r, int c, uint32_t tstride) {
+    uint32_t sw;
+    if constexpr (TL) {
+      sw = static_cast<uint32_t>(c >> 1) * tstride + static_cast<uint32_t>(c & 1) * (WT == W_INT4 ? 32u : 1024u);
+    } else {
+      (void)tstride;
+      sw = static_cast<uint32_t>(c) * (WT == W_INT4 ? 32u : 64u);
+    }
+    const uint32_t soff_w = __builtin_amdgcn_readfirstlane(sw);
+    constexpr uint32_t kSecond = TL ? 256u : 16u;  // FP8: the lane's second 16 K
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       u32x4_t* dst = j == 0 ? r.q0 : r.q1;
       dst[0] = bload<u32x4_t>(rs.w, o.w[j], soff_w);
-      if constexpr (WT == W_FP8) dst[1] = bload<u32x4_t>(rs.w, o.w[j] + 16u, soff_w);
+      if constexpr (WT == W_FP8) dst[1] = bload<u32x4_t>(rs.w, o.w[j] + kSecond, soff_w);
     }
   }
 
@@ -219,8 +240,14 @@ struct Wide {
           f[sh + 4] = __builtin_fmaf(static_cast<float>(v[1]), s, c);
         }
       }
+      if constexpr (TL) {
+        // Paired nibbles: f[sh] is K offset 2sh, f[sh + 4] is 2sh + 1.
 #pragma unroll
-      for (int e = 0; e < 4; ++e) p[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
+        for (int e = 0; e < 4; ++e) p[e] = pack_bf16x2(f[e], f[e + 4]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
+      }
     } else {
       (void)zsh;
 #pragma unroll
@@ -255,14 +282,14 @@ struct Wide {
   static __device__ __forceinline__ void unit(Smem& sm, int bc, int bn, int bd, int cnext2, bf16x8_t (&A)[MI],
                                               bf16x8_t (&B)[2], Raw& Rc, const Raw& Rn, const Rsrc& rs,
                                               const Offs& o, const uint32_t (&aoff)[4], f32x16_t (&acc)[MI][2],
-                                              int wave, uint32_t nm, uint32_t mg) {
+                                              int wave, uint32_t nm, uint32_t mg, uint32_t ts) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       if (t == 3) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
         dma_x(rs, o, sm, bd, cnext2, wave);
-        load_w(rs, o, Rc, cnext2);
+        load_w(rs, o, Rc, cnext2, ts);
         if constexpr (SHARE) {
           Rc.s0 = Rn.s0;
           Rc.s1 = Rn.s1;
@@ -425,9 +452,9 @@ struct Wide {
 // 64-wide halves of them), a.T = tiles, a.TM = tiles along M, a.U = T * G,
 // a.P = workgroups.  Tile t covers rows (t / (T/TM)) * 256 and
 // weight rows (t % (T/TM)) * 256.
-template <int WT, int SDT, bool SILU>
+template <int WT, int SDT, bool SILU, bool TL>
 __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
-  using W = Wide<WT, SDT, SILU>;
+  using W = Wide<WT, SDT, SILU, TL>;
   __shared__ typename W::Smem sm;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
@@ -448,6 +475,10 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
     rs.s = make_rsrc(a.scale, (static_cast<int64_t>((a.N - 1) / 128) * a.lds + a.K / 128) *
                                   (SDT == SCALE_F32 ? 4 : 2));
   }
+  // Tiled copy: N/16 tiles of TB bytes per 128-wide K chunk (wide_tiles_ok
+  // keeps the whole copy below 2^31 bytes).
+  const uint32_t ts = static_cast<uint32_t>(a.N / 16) * (WT == W_INT4 ? 1024u : 2048u);
+  if constexpr (TL) rs.w = make_rsrc(a.wtiles, static_cast<int64_t>(ts) * (a.K / 128));
 
   uint32_t aoff[4];
 #pragma unroll
@@ -474,8 +505,8 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
     const int c1 = cb + 1;
     W::dma_x(rs, o, sm, 0, cb, wave);
     W::dma_x(rs, o, sm, W::XB, c1, wave);
-    W::load_raw(rs, o, r0, cb);
-    W::load_raw(rs, o, r1, c1);
+    W::load_raw(rs, o, r0, cb, ts);
+    W::load_raw(rs, o, r1, c1, ts);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     bf16x8_t A[W::MI], B[2];
@@ -499,8 +530,8 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
     for (int q = 0; q < n; q += 2) {
       const int cn0 = cb + q + 2 < ce ? cb + q + 2 : ce - 1;
       const int cn1 = cb + q + 3 < ce ? cb + q + 3 : ce - 1;
-      W::template unit<false>(sm, b0, b1, b2, cn0, A, B, r0, r1, rs, o, aoff, acc, wave, nm, mg);
-      W::template unit<true>(sm, b1, b2, b0, cn1, A, B, r1, r0, rs, o, aoff, acc, wave, nm, mg);
+      W::template unit<false>(sm, b0, b1, b2, cn0, A, B, r0, r1, rs, o, aoff, acc, wave, nm, mg, ts);
+      W::template unit<true>(sm, b1, b2, b0, cn1, A, B, r1, r0, rs, o, aoff, acc, wave, nm, mg, ts);
       const int tb = b0;
       b0 = b2;
       b2 = b1;
@@ -515,9 +546,9 @@ __global__ __launch_bounds__(WD_THREADS, 1) void qgemm_wide_kernel(GemmArgs a) {
   }
 }
 
-template <int WT, int SDT, bool SILU = false>
+template <int WT, int SDT, bool SILU = false, bool TL = false>
 static hipError_t launch_wide_t(const GemmArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((qgemm_wide_kernel<WT, SDT, SILU>), dim3(a.P), dim3(WD_THREADS), 0, stream, a);
+  hipLaunchKernelGGL((qgemm_wide_kernel<WT, SDT, SILU, TL>), dim3(a.P), dim3(WD_THREADS), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -535,6 +566,11 @@ bool wide_ok(const GemmArgs& a, int wt) {
   return xb < lim && wb < lim && sb < lim && zb < lim;
 }
 
+bool wide_tiles_ok(const GemmArgs& a, int wt) {
+  const int64_t bytes = static_cast<int64_t>(a.N) * a.K / (wt == W_INT4 ? 2 : 1);
+  return a.wtiles != nullptr && a.N % 16 == 0 && a.K % 128 == 0 && bytes < (int64_t(1) << 31);
+}
+
 hipError_t launch_wide(int wt, const GemmArgs& a, hipStream_t stream) {
   if (wt == W_INT4 && a.silu_mul) {
     if (a.sdt == SCALE_BF16) return launch_wide_t<W_INT4, SCALE_BF16, true>(a, stream);
@@ -542,6 +578,16 @@ hipError_t launch_wide(int wt, const GemmArgs& a, hipStream_t stream) {
     return launch_wide_t<W_INT4, SCALE_F32, true>(a, stream);
   }
   if (a.silu_mul) return hipErrorInvalidValue;
+  if (a.wtiles != nullptr) {
+    if (wt == W_INT4) {
+      if (a.sdt == SCALE_BF16) return launch_wide_t<W_INT4, SCALE_BF16, false, true>(a, stream);
+      if (a.sdt == SCALE_F16) return launch_wide_t<W_INT4, SCALE_F16, false, true>(a, stream);
+      return launch_wide_t<W_INT4, SCALE_F32, false, true>(a, stream);
+    }
+    if (a.sdt == SCALE_BF16) return launch_wide_t<W_FP8, SCALE_BF16, false, true>(a, stream);
+    if (a.sdt == SCALE_F16) return launch_wide_t<W_FP8, SCALE_F16, false, true>(a, stream);
+    return launch_wide_t<W_FP8, SCALE_F32, false, true>(a, stream);
+  }
   if (wt == W_INT4) {
     if (a.sdt == SCALE_BF16) return launch_wide_t<W_INT4, SCALE_BF16>(a, stream);
     if (a.sdt == SCALE_F16) return launch_wide_t<W_INT4, SCALE_F16>(a, stream);

@@ -155,3 +155,51 @@ def test_tiled_row_split_qkv_m192(kind):
         wd = qo.decode_e4m3fn(data.numpy()[cols]) * scale.numpy()[(cols // 128)][:, np.arange(k) // 128]
         ref = qo.gemm_f64(x.float().numpy(), wd.astype(np.float32))
     tg.assert_gemm_close(y[:, cols], ref, what=f"tiled split {kind} M={m}")
+
+
+@pytest.mark.parametrize("kind,scale_dtype", [("int4", torch.bfloat16), ("int4", torch.float16),
+                                              ("int4", torch.float32), ("fp8", torch.float32),
+                                              ("fp8", torch.bfloat16)])
+@pytest.mark.parametrize("m,n,k", [(200, 2064, 2048), (300, 1040, 1280), (513, 784, 384)])
+def test_prefill_reads_tiles(kind, scale_dtype, m, n, k):
+    """Above 192 rows (129 on narrow outputs) the 256x256 prefill kernel reads
+    the tiled copy when one is given: its bits equal those of the same kernel
+    on the row-major weight (the same products in the same order), and the
+    result meets the oracle bar.  N here is a multiple of 16 but not of 256
+    (clamped tile rows) and K ranges end at odd 128-wide chunks."""
+    dev = tg._cuda()
+    rng = np.random.default_rng(m * 7 + n)
+    if kind == "int4":
+        w, x, xb, packed, scale, zero, _ = tg.int4_case(rng, m, n, k, dev, scale_dtype)
+        y0 = hs.awq_linear(x, w)
+        y1 = hs.awq_linear(x, tile_int4_weight(w))
+        ref = tg.int4_ref(xb, packed, scale, zero, n, k)
+    else:
+        w, x, xb, data, scale = tg.fp8_case(rng, m, n, k, dev, scale_dtype)
+        y0 = hs.fp8_linear(x, w)
+        y1 = hs.fp8_linear(x, tile_fp8_weight(w))
+        ref = tg.fp8_ref(xb, data, scale, n, k)
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16)), f"{kind} tiled prefill bits differ"
+    tg.assert_gemm_close(y1, ref, what=f"tiled prefill {kind} M={m}")
+
+
+@pytest.mark.parametrize("kind", ["int4", "fp8"])
+def test_prefill_reads_tiles_baseline_gate_up(kind):
+    """BASELINE gate_up (34816 x 5120) at 2048 rows: tiled and row-major
+    weights give identical bits (split tiles settled across workgroups)."""
+    dev = tg._cuda()
+    n, k, m = 34816, 5120, 2048
+    g = torch.Generator(device="cpu").manual_seed(2048)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(dev)
+    if kind == "int4":
+        packed, zero, scale, _ = _int4_full(n, k, 1, 2049)
+        w = hs.PackedInt4Weight(packed.to(dev), scale.to(dev), zero.to(dev), (n, k))
+        y0, y1 = hs.awq_linear(x, w), hs.awq_linear(x, tile_int4_weight(w))
+    else:
+        data = torch.randint(0, 256, (n, k), generator=g, dtype=torch.int32).to(torch.uint8)
+        data[(data & 0x7F) == 0x7F] = 0x00
+        scale = torch.rand(n // 128, k // 128, generator=g) * 0.099 + 0.001
+        w = hs.BlockScaledFP8Weight(data.to(dev).view(torch.float8_e4m3fn), scale.to(dev), (n, k))
+        y0, y1 = hs.fp8_linear(x, w), hs.fp8_linear(x, tile_fp8_weight(w))
+    assert torch.isfinite(y0.float()).all()
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
