@@ -18,7 +18,8 @@ an FP8 tile the bytes are ordered so that each of a lane's two 16-byte loads
 is one contiguous KiB across the wave (two halves of 64 K each; the 16 bytes
 of row r at K quarter p of a half at (16p + r) * 16).  The copy is made once, at load time, and
 the row-major tensors stay in the weight (every other kernel reads them, and
-the tiled kernel only takes activations of at most 64 rows); the values are
+the tiled decode kernel only takes activations of at most 64 rows, the
+256x256 prefill kernel reads the tiles above that); the values are
 not changed (tests check the round trip and the GEMM results).
 
 TiledInt4Weight / TiledFP8Weight are the reference's dataclasses with one

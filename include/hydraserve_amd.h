@@ -134,8 +134,9 @@ int hs_fp8_gemm(const void* x, int64_t ldx,
  * of the tile (data.view(N/16, 16, K/128, 2, 4, 16).permute(2, 0, 3, 4, 1, 5)).
  * Requires N % 16 == 0 and K % 128 == 0 for the tiles to be read; the
  * row-major weight is still passed and used by the kernels that do not read
- * tiles (the tiles serve the block-major decode kernel at 1..16 rows, where
- * one load instruction then reads one contiguous tile).  Results are those of
+ * tiles (the tiles serve the tiled decode kernel at 1..64 rows, where one
+ * load instruction then reads one contiguous tile, and the 256x256 prefill
+ * kernel above that, whose loads then touch fewer cache lines).  Results are those of
  * the untiled entry points to the same bars. */
 int hs_int4_gemm_tiled(const void* x, int64_t ldx,
                        const int32_t* packed, int64_t ld_packed, const int32_t* tiles,
