@@ -100,6 +100,7 @@ PMC_TRAFFIC_KIB = {
     ("int4", "down", 16, "row-major"): (26201.5, 1452.5),
     ("int4", "gate_up", 64, "tiled"): (49033.0, 4352.0),
     ("int4", "gate_up", 1, "tiled"): (46148.8, 68.0),
+    ("int4", "gate_up", 2048, "tiled"): (604139.4, 312730.8),
 }
 FETCH_CAL, WRITE_CAL = 2.0, 1.0
 
@@ -530,7 +531,7 @@ def main():
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": dom_p["roofline_frac"],
-            "traffic": None,
+            "traffic": pmc_traffic(dom_p["kind"], dom_p["shape"], dom_p["M"], args.layout),
             "kernel": f"{dom_p['kind'].upper()} prefill {dom_p['shape']} M={dom_p['M']} ({dom_p['N']}x{dom_p['K']}), "
             f"{args.layout} weights",
             "flops_per_launch": 2 * dom_p["M"] * dom_p["N"] * dom_p["K"],
