@@ -608,34 +608,37 @@ def profile(torch, gen, dev, spec, launches):
 
 
 def sweep(torch, gen, dev):
-    """gate_up followed by SiLU-and-mul: fused epilogue vs the reference's sequence."""
+    """gate_up followed by SiLU-and-mul: fused epilogue vs the reference's
+    sequence, on the checkpoint tensors and on the load-time tiled copies."""
     out = []
     # gate_up followed by SiLU-and-mul: fused epilogue on the interleaved
     # weight vs the reference's sequence (GEMM, chunk, activation launch).
-    from hydraserve_amd.kernels import awq_gate_up_silu_mul, interleave_gate_up, silu_and_mul
+    import hydraserve_amd as hs
+    from hydraserve_amd.kernels import awq_gate_up_silu_mul, interleave_gate_up, silu_and_mul, tile_int4_weight
 
     per_copy = int4_bytes(*GATE_UP)
     ws = make_int4(torch, *GATE_UP, copies_for(per_copy), gen, dev)
     wis = [interleave_gate_up(w) for w in ws]
+    weights = {"": (ws, wis), "_tiled": ([tile_int4_weight(w) for w in ws], [tile_int4_weight(w) for w in wis])}
     for m in (1, 4, 16, 64, 128, 2048):
         x = torch.randn(m, GATE_UP[1], generator=gen, device=dev).to(torch.bfloat16)
+        r = {"kind": "int4", "shape": "gate_up+silu_and_mul", "M": m, "N": GATE_UP[0], "K": GATE_UP[1]}
+        for tag, (wp, wf) in weights.items():
 
-        def unfused(i):
-            import hydraserve_amd as hs
+            def unfused(i, wp=wp):
+                gate, up = hs.awq_linear(x, wp[i % len(wp)]).chunk(2, dim=-1)
+                return silu_and_mul(gate.contiguous(), up.contiguous())
 
-            gate, up = hs.awq_linear(x, ws[i % len(ws)]).chunk(2, dim=-1)
-            return silu_and_mul(gate.contiguous(), up.contiguous())
+            def fused(i, wf=wf):
+                return awq_gate_up_silu_mul(x, wf[i % len(wf)])
 
-        def fused(i):
-            return awq_gate_up_silu_mul(x, wis[i % len(wis)])
-
-        ms_u, _ = graph_time_ms(torch, unfused, 10, len(ws))
-        ms_f, _ = graph_time_ms(torch, fused, 10, len(ws))
-        r = {"kind": "int4", "shape": "gate_up+silu_and_mul", "M": m, "N": GATE_UP[0], "K": GATE_UP[1],
-             "unfused_us": round(ms_u * 1e3, 2), "fused_us": round(ms_f * 1e3, 2)}
+            ms_u, _ = graph_time_ms(torch, unfused, 10, len(wp))
+            ms_f, _ = graph_time_ms(torch, fused, 10, len(wf))
+            r[f"unfused{tag}_us"] = round(ms_u * 1e3, 2)
+            r[f"fused{tag}_us"] = round(ms_f * 1e3, 2)
         print(json.dumps(r), file=sys.stderr, flush=True)
         out.append(r)
-    del ws, wis
+    del ws, wis, weights
     torch.cuda.empty_cache()
     return out
 

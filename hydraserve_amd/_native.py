@@ -32,6 +32,8 @@ SIGNATURES = {
     "hs_int4_gemm": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _I64, _P]),
     "hs_int4_gemm_noalloc": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
     "hs_int4_gemm_silu_mul": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _I64, _P]),
+    "hs_int4_gemm_silu_mul_tiled": (
+        _I, [_P, _I64, _P, _I64, _P, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _I64, _P]),
     "hs_fp8_gemm": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _I, _I, _I, _P, _I64, _P]),
     "hs_int4_gemm_tiled": (_I, [_P, _I64, _P, _I64, _P, _P, _I64, _I, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _I64, _P]),
     "hs_fp8_gemm_tiled": (_I, [_P, _I64, _P, _I64, _P, _P, _I64, _I, _P, _I64, _I, _I, _I, _P, _I64, _P]),
@@ -155,9 +157,10 @@ def int4_gemm(x, packed, scale, zero_point, n: int, k: int, group: int, tiles=No
     return y
 
 
-def int4_gemm_silu_mul(x, packed, scale, zero_point, n: int, k: int, group: int):
+def int4_gemm_silu_mul(x, packed, scale, zero_point, n: int, k: int, group: int, tiles=None):
     """silu(gate) * up [M, N/2] (bf16) on a gate/up-interleaved weight of N rows,
-    or None where the fused kernel does not apply (HS_EUNSUPPORTED)."""
+    or None where the fused kernel does not apply (HS_EUNSUPPORTED)
+    (``tiles``: the load-time tiled copy of the interleaved packed words)."""
     import torch
 
     m = x.shape[0]
@@ -168,8 +171,11 @@ def int4_gemm_silu_mul(x, packed, scale, zero_point, n: int, k: int, group: int)
     stream = torch.cuda.current_stream(x.device).cuda_stream
     need = L.hs_gemm_workspace_bytes(HS_KIND_INT4, m, n, k)
     ws = workspaces.get(x.device, stream, need)
-    rc = L.hs_int4_gemm_silu_mul(
-        x.data_ptr(), x.stride(0), packed.data_ptr(), packed.stride(0),
+    name = "hs_int4_gemm_silu_mul" if tiles is None else "hs_int4_gemm_silu_mul_tiled"
+    w_args = (packed.data_ptr(), packed.stride(0)) if tiles is None else (
+        packed.data_ptr(), packed.stride(0), tiles.data_ptr())
+    rc = getattr(L, name)(
+        x.data_ptr(), x.stride(0), *w_args,
         scale.data_ptr(), scale.stride(0), dtype_code(scale.dtype),
         zero_point.data_ptr(), zero_point.stride(0),
         y.data_ptr(), y.stride(0), m, n, k, group,
@@ -177,7 +183,7 @@ def int4_gemm_silu_mul(x, packed, scale, zero_point, n: int, k: int, group: int)
     )
     if rc == HS_EUNSUPPORTED:
         return None
-    check(rc, "hs_int4_gemm_silu_mul")
+    check(rc, name)
     return y
 
 

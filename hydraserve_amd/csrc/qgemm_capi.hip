@@ -188,7 +188,9 @@ struct TmPlan {
   int64_t ws_bytes = 0;
 };
 
-TmPlan tm_plan(int wt, int M, int N, int K) {
+// silu: the fused SiLU store pairs tiles 2k and 2k+1 inside one group, so
+// groups hold an even number of tiles.
+TmPlan tm_plan(int wt, int M, int N, int K, bool silu = false) {
   TmPlan best;
   const int cus = device_cus();
   const Tuning& tn = tuning();
@@ -210,6 +212,10 @@ TmPlan tm_plan(int wt, int M, int N, int K) {
     const int S = static_cast<int>(cdiv(NC, cps));
     int tpw = tn.tm_tpw > 0 ? tn.tm_tpw : static_cast<int>(cdiv(NT * S, cus));
     if (tpw < 1) tpw = 1;
+    if (silu && tpw % 2 != 0) {
+      if (tn.tm_tpw > 0) continue;
+      ++tpw;
+    }
     if (tpw > tm_max_tpw(wt, M)) continue;
     const int64_t groups = cdiv(NT, tpw);
     const int64_t P = groups * S;
@@ -612,8 +618,10 @@ int64_t hs_gemm_workspace_bytes(int kind, int M, int N, int K) {
           }
   // the tiled decode kernel (calls that pass a tiled copy)
   if (M <= 64 && N % 16 == 0 && K % 128 == 0) {
-    const int64_t b = hsq::tm_plan(kind, M, N, K).ws_bytes;
-    best = b > best ? b : best;
+    for (int silu = 0; silu < 2; ++silu) {
+      const int64_t b = hsq::tm_plan(kind, M, N, K, silu != 0).ws_bytes;
+      best = b > best ? b : best;
+    }
   }
   // the two row halves of the narrow-output split at 129..256 rows
   if (M > 128 && M <= 256 && (N < K || M <= 192)) {
@@ -694,10 +702,10 @@ int hs_int4_gemm_noalloc(const void* x, int64_t ldx, const int32_t* packed, int6
   return rc == HS_EWORKSPACE ? HS_ESCRATCH : rc;
 }
 
-int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,
-                          int64_t ld_scale, int scale_dtype, const int32_t* zero_point, int64_t ld_zero, void* y,
-                          int64_t ldy, int M, int N, int K, int group, void* workspace, int64_t workspace_bytes,
-                          void* stream) {
+static int int4_silu_impl(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed,
+                          const int32_t* tiles, const void* scale, int64_t ld_scale, int scale_dtype,
+                          const int32_t* zero_point, int64_t ld_zero, void* y, int64_t ldy, int M, int N, int K,
+                          int group, void* workspace, int64_t workspace_bytes, void* stream) {
   if (M < 0 || N < 0 || K < 0) return HS_EINVAL;
   if (group != 128) return HS_EUNSUPPORTED;
   if (N % 32 != 0) return HS_EINVAL;
@@ -727,6 +735,27 @@ int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int
   a.tune = hsq::tuning().tune;
   a.silu_mul = 1;
   if (!hsq::extents_ok(hsq::W_INT4, a, N / 2)) return HS_EUNSUPPORTED;
+  // Tiled copy of the interleaved weight: the tiled decode kernel's store
+  // carries the epilogue up to 64 rows, the 256x256 prefill kernel reads the
+  // tiles from 129 rows; 17..128 rows and every other case use the kernels
+  // below on the row-major weight.
+  const int32_t* const tl = tiles != nullptr && hsq::aligned16(tiles) && K % 128 == 0 && N % 16 == 0 ? tiles : nullptr;
+  if (tl != nullptr) {
+    a.wtiles = tl;
+    if (hsq::tm_min_ok(hsq::W_INT4, M, N, K) && hsq::tiled_ok(a, hsq::W_INT4)) {
+      const hsq::TmPlan tp = hsq::tm_plan(hsq::W_INT4, M, N, K, true);
+      if (tp.P > 0) {
+        if (tp.splits > 1 && (workspace == nullptr || workspace_bytes < tp.ws_bytes)) return HS_EWORKSPACE;
+        a.tpw = tp.tpw;
+        a.splits = tp.splits;
+        a.cps = tp.cps;
+        a.counters = reinterpret_cast<int*>(workspace);
+        a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + hsq::kCounterBytes);
+        return hsq::hip_code(hsq::launch_tiled(hsq::W_INT4, a, static_cast<hipStream_t>(stream)));
+      }
+    }
+    a.wtiles = nullptr;
+  }
   // The fused epilogue is in the block-major GEMV kernel (1..16 rows, X in
   // LDS) and in the 17..128-row LDS-DMA kernel.
   if (M <= 16) {
@@ -752,6 +781,10 @@ int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int
   if (M > 128) {
     // Prefill: the 256x256-tile kernel's store carries the epilogue.
     if (!hsq::wide_ok(a, hsq::W_INT4)) return HS_EUNSUPPORTED;
+    if (tl != nullptr && !hsq::tuning().wide_tiles_off) {
+      a.wtiles = tl;
+      if (!hsq::wide_tiles_ok(a, hsq::W_INT4)) a.wtiles = nullptr;
+    }
     const hsq::Plan p = hsq::make_plan(hsq::W_INT4, M, N, K, false, false, true, false, false);
     if (!p.wide || p.T > hsq::kMaxTiles) return HS_EUNSUPPORTED;
     if (workspace == nullptr || workspace_bytes < p.ws_bytes) return HS_EWORKSPACE;
@@ -779,6 +812,22 @@ int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int
   a.counters = reinterpret_cast<int*>(workspace);
   a.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.counter_bytes);
   return hsq::hip_code(hsq::launch_mid(hsq::W_INT4, a, p.BMI, p.NJ, p.NW, static_cast<hipStream_t>(stream)));
+}
+
+int hs_int4_gemm_silu_mul(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed, const void* scale,
+                          int64_t ld_scale, int scale_dtype, const int32_t* zero_point, int64_t ld_zero, void* y,
+                          int64_t ldy, int M, int N, int K, int group, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
+  return int4_silu_impl(x, ldx, packed, ld_packed, nullptr, scale, ld_scale, scale_dtype, zero_point, ld_zero, y, ldy,
+                        M, N, K, group, workspace, workspace_bytes, stream);
+}
+
+int hs_int4_gemm_silu_mul_tiled(const void* x, int64_t ldx, const int32_t* packed, int64_t ld_packed,
+                                const int32_t* tiles, const void* scale, int64_t ld_scale, int scale_dtype,
+                                const int32_t* zero_point, int64_t ld_zero, void* y, int64_t ldy, int M, int N, int K,
+                                int group, void* workspace, int64_t workspace_bytes, void* stream) {
+  return int4_silu_impl(x, ldx, packed, ld_packed, tiles, scale, ld_scale, scale_dtype, zero_point, ld_zero, y, ldy,
+                        M, N, K, group, workspace, workspace_bytes, stream);
 }
 
 static int fp8_gemm_impl(const void* x, int64_t ldx, const uint8_t* data, int64_t ld_data, const uint8_t* tiles,

@@ -134,6 +134,49 @@ constexpr int tm_steps_mod(int lo, int hi, int R, int r = 0) {
 // a chunk's X fragments from LDS and dequantises half of each of its tiles,
 // and the two halves of a set run on different SIMDs.  The K-half-1 partial
 // sums are added to the K-half-0 ones through LDS at the end.
+// Fused SiLU-and-mul store of a tile group (a.silu_mul, INT4 gate_up with
+// rows interleaved in 16-row blocks, so tile 2k holds gate rows and tile
+// 2k + 1 the matching up rows; the plan keeps groups at an even tile count
+// from an even first tile).  Every wave puts its final tile values into the
+// freed X buffers at the tile's local index, then the owner of each gate
+// tile reads the up values of the same (row, column) from the next local
+// tile and stores bf16(g * sigmoid(g) * u), g and u rounded to bf16 first as
+// the reference's unfused sequence does (hydraserve/model/runtime.py:1202-1210,
+// silu_and_mul at hydraserve/kernels/activation.py:66-76), into y [M, N/2].
+template <int MB, int TW, int NG>
+__device__ __forceinline__ void tiled_silu_store(const GemmArgs& a, uint8_t* lds, const f32x4_t (&v)[TW][MB],
+                                                 const int (&tt)[TW], int nto, int kg, int lane) {
+  const int n = lane & 15, p4 = lane >> 4;
+  f32x4_t* st = reinterpret_cast<f32x4_t*>(lds);
+  __syncthreads();  // every wave is done with the X buffers
+#pragma unroll
+  for (int i = 0; i < TW; ++i) {
+    if (i >= nto) continue;
+#pragma unroll
+    for (int b = 0; b < MB; ++b) st[((kg + NG * i) * MB + b) * 64 + lane] = v[i][b];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TW; ++i) {
+    if (i >= nto || (tt[i] & 1) != 0) continue;
+    const int col = 8 * tt[i] + n;  // output column 16 (tt / 2) + n
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      const f32x4_t up = st[((kg + NG * i + 1) * MB + b) * 64 + lane];
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const int m = 16 * b + 4 * p4 + e2;
+        if (m < a.M) {
+          const float gv = bf16_to_f32(to_bf16_bits(v[i][b][e2]));
+          const float uv = bf16_to_f32(to_bf16_bits(up[e2]));
+          const float sig = 1.0f / (1.0f + expf(-gv));
+          a.y[static_cast<int64_t>(m) * a.ldy + col] = to_bf16_bits(gv * sig * uv);
+        }
+      }
+    }
+  }
+}
+
 template <int WT, int SDT, int MB, int TW, int NW, bool KS = false>
 __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
   using C = Tm<WT, MB, TW, NW>;
@@ -508,8 +551,15 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
     }
   }
 
+  static_assert(NG * TW * MB * 64 * 16 <= 2 * C::XR, "a group's final tiles fit the X buffers");
   // Lane (n, p4), register e of block (i, b): row 16b + 4p4 + e, column 16 tt[i] + n.
   if (a.splits == 1) {
+    if constexpr (WT == W_INT4) {
+      if (a.silu_mul) {
+        tiled_silu_store<MB, TW, NG>(a, &sm.xs[0][0], acc, tt, nto, kg, lane);
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < TW; ++i) {
       if (i >= nto) continue;
@@ -569,17 +619,26 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_tiled_kernel(GemmArgs a) {
       }
     }
   }
+  bool fused = false;
+  if constexpr (WT == W_INT4) {
+    if (a.silu_mul) {
+      tiled_silu_store<MB, TW, NG>(a, &sm.xs[0][0], sum, tt, nto, kg, lane);
+      fused = true;
+    }
+  }
+  if (!fused) {
 #pragma unroll
-  for (int i = 0; i < TW; ++i) {
-    if (i >= nto) continue;
-    const int col = 16 * tt[i] + n;
+    for (int i = 0; i < TW; ++i) {
+      if (i >= nto) continue;
+      const int col = 16 * tt[i] + n;
 #pragma unroll
-    for (int b = 0; b < MB; ++b)
+      for (int b = 0; b < MB; ++b)
 #pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        const int m = 16 * b + 4 * p4 + e2;
-        if (m < a.M) a.y[static_cast<int64_t>(m) * a.ldy + col] = to_bf16_bits(sum[i][b][e2]);
-      }
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int m = 16 * b + 4 * p4 + e2;
+          if (m < a.M) a.y[static_cast<int64_t>(m) * a.ldy + col] = to_bf16_bits(sum[i][b][e2]);
+        }
+    }
   }
   reset_counter(a.counters, g);
 }
@@ -621,8 +680,9 @@ int tm_slot_floats(int wt, int M) { return tm_nw(wt, M) * tm_tw(wt, M) * tm_mb(M
 // Tiled copy present, M <= 64, N a multiple of 16, K a multiple of 128, every
 // buffer range below 2^31 bytes; INT4 scale rows 4-byte aligned.
 bool tiled_ok(const GemmArgs& a, int wt) {
-  if (a.wtiles == nullptr || a.M <= 0 || a.M > 64 || a.N % 16 != 0 || a.K % 128 != 0 || a.silu_mul || !a.xvec)
-    return false;
+  if (a.wtiles == nullptr || a.M <= 0 || a.M > 64 || a.N % 16 != 0 || a.K % 128 != 0 || !a.xvec) return false;
+  // fused SiLU: INT4, gate/up 16-row blocks in tile pairs
+  if (a.silu_mul && (wt != W_INT4 || a.N % 32 != 0)) return false;
   if ((reinterpret_cast<uintptr_t>(a.scale) & 3) != 0 || (reinterpret_cast<uintptr_t>(a.wtiles) & 15) != 0) return false;
   if (wt == W_INT4) {
     // a round's scales and zero points go by 16-byte loads from 4-byte
@@ -659,6 +719,7 @@ static hipError_t launch_tiled_s(const GemmArgs& a, hipStream_t stream) {
 
 hipError_t launch_tiled(int wt, const GemmArgs& a, hipStream_t stream) {
   if (a.tpw <= 0 || a.tpw > tm_max_tpw(wt, a.M) || a.splits <= 0 || a.cps <= 0) return hipErrorInvalidValue;
+  if (a.silu_mul && (wt != W_INT4 || a.tpw % 2 != 0 || a.N % 32 != 0)) return hipErrorInvalidValue;
   if (wt == W_INT4) {
     if (a.sdt == SCALE_BF16) return launch_tiled_s<W_INT4, SCALE_BF16>(a, stream);
     if (a.sdt == SCALE_F16) return launch_tiled_s<W_INT4, SCALE_F16>(a, stream);

@@ -572,6 +572,11 @@ bool wide_tiles_ok(const GemmArgs& a, int wt) {
 }
 
 hipError_t launch_wide(int wt, const GemmArgs& a, hipStream_t stream) {
+  if (wt == W_INT4 && a.silu_mul && a.wtiles != nullptr) {
+    if (a.sdt == SCALE_BF16) return launch_wide_t<W_INT4, SCALE_BF16, true, true>(a, stream);
+    if (a.sdt == SCALE_F16) return launch_wide_t<W_INT4, SCALE_F16, true, true>(a, stream);
+    return launch_wide_t<W_INT4, SCALE_F32, true, true>(a, stream);
+  }
   if (wt == W_INT4 && a.silu_mul) {
     if (a.sdt == SCALE_BF16) return launch_wide_t<W_INT4, SCALE_BF16, true>(a, stream);
     if (a.sdt == SCALE_F16) return launch_wide_t<W_INT4, SCALE_F16, true>(a, stream);

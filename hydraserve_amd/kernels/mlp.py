@@ -107,6 +107,9 @@ def awq_gate_up_silu_mul(hidden, weight: PackedInt4Weight):
     ):
         raise ValueError("packed INT4 tensors must be contiguous CUDA tensors")
     _check_int4_storage(weight)
+    tiles = getattr(weight, "tiles", None)  # load-time tiled copy (kernels/tiles.py)
+    if tiles is not None and not (tiles.is_cuda and tiles.device == hidden.device and tiles.is_contiguous()):
+        raise ValueError("INT4 weight tiles must be a contiguous tensor on the activation's GPU")
     import torch
 
     flattened = hidden.reshape(-1, k).contiguous()
@@ -120,7 +123,7 @@ def awq_gate_up_silu_mul(hidden, weight: PackedInt4Weight):
         # Dynamo/Inductor: the opaque custom op (hydraserve_amd/ops.py)
         return torch.ops.hydraserve_amd.int4_gate_up_silu_mul(*args).reshape(shape)
     with device_guard(hidden.device):
-        out = _native.int4_gemm_silu_mul(*args)
+        out = _native.int4_gemm_silu_mul(*args, tiles=tiles)
         if out is None:
             out = unfused_gate_up_silu_mul(*args)
     return out.reshape(shape)

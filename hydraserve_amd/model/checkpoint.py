@@ -149,9 +149,9 @@ def load_linear_weights(
     ``fuse_gate_up``: for each ``<p>.gate_proj.weight`` / ``<p>.up_proj.weight``
     pair, also ``<p>.gate_up_proj.weight`` (fused along N) and, for INT4,
     ``<p>.gate_up_proj.weight.interleaved`` (the fused SiLU kernel's layout).
-    ``tile``: device-resident INT4/FP8 weights (N % 16 == 0, K % 128 == 0) come
-    with the load-time tiled copy the block-major decode kernel reads
-    (kernels/tiles.py).
+    ``tile``: device-resident INT4/FP8 weights (N % 16 == 0, K % 128 == 0),
+    the interleaved gate_up included, come with the load-time tiled copy the
+    tiled decode and 256x256 prefill kernels read (kernels/tiles.py).
     """
     from ..kernels.mlp import interleave_gate_up
     from ..kernels.tiles import tile_fp8_weight, tile_int4_weight
@@ -175,8 +175,6 @@ def load_linear_weights(
                 out[f"{stem}.gate_up_proj.weight.interleaved"] = interleave_gate_up(fused)
     if tile:
         for name, w in list(out.items()):
-            if name.endswith(".interleaved"):
-                continue
             n_k = getattr(w, "original_shape", None)
             if n_k is None or n_k[0] % 16 or n_k[1] % 128:
                 continue

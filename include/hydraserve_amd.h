@@ -112,6 +112,23 @@ int hs_int4_gemm_silu_mul(const void* x, int64_t ldx,
                           void* workspace, int64_t workspace_bytes,
                           void* stream);
 
+/* hs_int4_gemm_silu_mul with a load-time tiled copy of the interleaved
+ * gate_up weight (layout as for hs_int4_gemm_tiled; same fused branch,
+ * hydraserve/model/runtime.py:1202-1210).  Up to 64 rows the tiled decode
+ * kernel's store carries the activation (each 16-row gate tile and the up
+ * tile after it are settled in one workgroup); from 129 rows the 256x256
+ * prefill kernel reads the tiles; 17..128 rows and shapes the tiled kernels
+ * do not take run as hs_int4_gemm_silu_mul on the row-major weight.  Results
+ * are those of hs_int4_gemm_silu_mul to the same bars. */
+int hs_int4_gemm_silu_mul_tiled(const void* x, int64_t ldx,
+                                const int32_t* packed, int64_t ld_packed, const int32_t* tiles,
+                                const void* scale, int64_t ld_scale, int scale_dtype,
+                                const int32_t* zero_point, int64_t ld_zero,
+                                void* y, int64_t ldy,
+                                int M, int N, int K, int group,
+                                void* workspace, int64_t workspace_bytes,
+                                void* stream);
+
 /* Y[M,N] = X[M,K] . (decode(W) * scale_inv[n/128, k/128])^T, fp32 accumulation,
  * bf16 output.  Replaces the GPU branch of fp8_linear
  * (hydraserve/kernels/fp8.py:24-97, Triton kernel fp8.py:104-168). */

@@ -7,7 +7,10 @@ process), so every case below goes through the tiled kernel: every row-block
 count (1..64 rows, partial blocks; 129..192 rows split into 128 row-major
 rows and a tiled rest), waves holding 0..2 tiles (N = 64: four
 tiles), K ranges split across workgroups, all scale dtypes.  The checks are
-those of tests/test_gemm_gpu.py, plus a bit-identical second call.
+those of tests/test_gemm_gpu.py, plus a bit-identical second call.  The
+"silu" cases run the fused gate_up SiLU-and-mul store of the tiled kernel
+(awq_gate_up_silu_mul on the tiled copy of an interleaved weight) against
+silu(bf16(gate)) * bf16(up) from the oracle GEMM, as tests/test_mlp.py does.
 """
 
 from __future__ import annotations
@@ -18,7 +21,8 @@ import torch
 from tests import test_gemm_gpu as tg
 
 import hydraserve_amd as hs
-from hydraserve_amd.kernels import tile_fp8_weight, tile_int4_weight
+from hydraserve_amd.kernels import awq_gate_up_silu_mul, interleave_gate_up, tile_fp8_weight, tile_int4_weight
+from oracle import quant_oracle as qo
 
 # (kind, M, N, K, scale dtype)
 CASES = (
@@ -34,7 +38,27 @@ CASES = (
     # 129..192 rows: 128 rows row-major, the rest through the tiled kernel
     + [("int4", 160, 4096, 1024, torch.bfloat16), ("fp8", 192, 4096, 2048, torch.float32),
        ("int4", 190, 1024, 4096, torch.float16)]
+    # fused SiLU store: 1..64 rows (each row-block count, the K-half pairing
+    # at 33..64), 68 tiles of 10 chunks (an odd tile count per wave set, a
+    # ragged last group), 4 tiles; fp16 / fp32 scales
+    + [("silu", m, n, k, torch.bfloat16) for m in (1, 5, 16, 17, 33, 64)
+       for n, k in ((2048, 1024), (1088, 1280), (64, 384))]
+    + [("silu", m, 2048, 2048, sdt) for m in (8, 64) for sdt in (torch.float16, torch.float32)]
 )
+
+
+def _silu_ref(y, n):
+    """silu(bf16(gate)) * bf16(up) in float64 from a GEMM result (and its
+    exact-weight variant) on the original, non-interleaved weight."""
+
+    def act(yy):
+        gu = qo.bf16_bits_to_f32(qo.f32_to_bf16_bits(np.asarray(yy, dtype=np.float32))).astype(np.float64)
+        g, u = gu[:, : n // 2], gu[:, n // 2 :]
+        return g / (1.0 + np.exp(-g)) * u
+
+    ref = act(y).view(tg.RefArray)
+    ref.exact = act(y.exact)
+    return ref
 
 
 def main() -> int:
@@ -43,7 +67,13 @@ def main() -> int:
         rng = np.random.default_rng(31 * m + n + i)
         what = f"tiled {kind} M={m} N={n} K={k} {sdt}"
         print(what, flush=True)
-        if kind == "int4":
+        if kind == "silu":
+            w, x, xb, packed, scale, zero, _ = tg.int4_case(rng, m, n, k, dev, sdt)
+            wt = tile_int4_weight(interleave_gate_up(w))
+            y = awq_gate_up_silu_mul(x, wt)
+            y2 = awq_gate_up_silu_mul(x, wt)
+            ref = _silu_ref(tg.int4_ref(xb, packed, scale, zero, n, k), n)
+        elif kind == "int4":
             w, x, xb, packed, scale, zero, _ = tg.int4_case(rng, m, n, k, dev, sdt)
             wt = tile_int4_weight(w)
             y = hs.awq_linear(x, wt)

@@ -146,13 +146,17 @@ def _check_fused(m, n, k, scale_dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("tiled", [False, True])
 @pytest.mark.parametrize("m", [1, 8, 16, 64, 2048])
-def test_fused_gate_up_silu_mul_full_shape(m):
+def test_fused_gate_up_silu_mul_full_shape(m, tiled):
     """The benchmarked shape, gate_up 5120 -> 34816: at 1..16 rows the
     block-major kernel's largest row partitions and the row-partitioned
     kernel's widest SiLU instance, at 64 the streaming kernel's two-column-block
-    store, at 2048 the prefill SiLU instance.  The oracle recomputes gate and up
-    for the output columns of test_gemm_gpu._tile_columns (every tile)."""
+    store, at 2048 the prefill SiLU instance.  ``tiled``: the tiled copy of the
+    interleaved weight, read by the tiled decode kernel's fused store up to 64
+    rows and by the prefill SiLU instance's tiled loads at 2048.  The oracle
+    recomputes gate and up for the output columns of
+    test_gemm_gpu._tile_columns (every tile)."""
     if not torch.cuda.is_available():
         pytest.skip("needs a ROCm GPU")
     from hydraserve_amd.kernels import awq_gate_up_silu_mul
@@ -172,7 +176,14 @@ def test_fused_gate_up_silu_mul_full_shape(m):
     wi = interleave_gate_up(w)
     from hydraserve_amd import _native
 
-    assert _native.int4_gemm_silu_mul(x.to(dev), wi.packed, wi.scale, wi.zero_point, n, k, 128) is not None
+    if tiled:
+        from hydraserve_amd.kernels import tile_int4_weight
+
+        wi = tile_int4_weight(wi)
+        assert _native.int4_gemm_silu_mul(
+            x.to(dev), wi.packed, wi.scale, wi.zero_point, n, k, 128, tiles=wi.tiles) is not None
+    else:
+        assert _native.int4_gemm_silu_mul(x.to(dev), wi.packed, wi.scale, wi.zero_point, n, k, 128) is not None
     out = awq_gate_up_silu_mul(x.to(dev), wi).cpu()
     assert out.shape == (m, half)
     cols = tg._tile_columns(half, m)
