@@ -222,14 +222,29 @@ TmPlan tm_plan(int wt, int M, int N, int K, bool silu = false) {
     if (P > 4 * cus || groups > kMaxTiles) continue;
     const double waves_per_cu = P > cus ? static_cast<double>(cdiv(P, cus)) : 1.0;
     const int tw = (tpw + 3) / 4;  // tiles per SIMD
-    const double mem = tpw * tb + 0.5 * mb * 4096.0;
+    // At one row block a wave streams its tiles at ~1/6 of what the
+    // workgroup's eight waves stream together, so the busiest wave's tile
+    // count bounds the workgroup's pace too, and each K range pays its ring
+    // fill (~3 INT4 / 2 FP8 chunks) once.  Fitted to the best of a measured
+    // sweep at 1..16 rows: down 17408->5120 at 6 K ranges of 8-tile groups
+    // (INT4 15.8-16.1 us against 16.7-17.0 at 8 ranges of 10-tile groups,
+    // where two waves hold two tiles); qkv 5120->10240 INT4 at 3 ranges, 12.2
+    // against 13.6 us at 5 ranges of 8 chunks.
+    double wbytes = tpw * tb;
+    double fill = 0.0;
+    if (mb == 1) {
+      const double wave_bound = ((tpw + 7) / 8) * 6.0 * tb;
+      wbytes = wave_bound > wbytes ? wave_bound : wbytes;
+      fill = wt == W_INT4 ? 3.0 : 2.0;
+    }
+    const double mem = wbytes + 0.5 * mb * 4096.0;
     const double cmp = tw * comp;
     // a split group settles after its last K range: partial stores, the
     // arrival, then coherent loads of four contributors per round trip; the
     // partials grow with the row blocks (measured at 64 rows: o_proj
     // 8192->5120 19.2 us at 4 K ranges against 22.9 at 8)
     const double settle = S > 1 ? (30000.0 + 20000.0 * ((S + 3) / 4)) * mb : 0.0;
-    const double est = waves_per_cu * cps * (mem > cmp ? mem : cmp) + settle;
+    const double est = waves_per_cu * (cps + fill) * (mem > cmp ? mem : cmp) + settle;
     if (est < best_est) {
       best_est = est;
       best.tpw = tpw;
