@@ -101,6 +101,7 @@ PMC_TRAFFIC_KIB = {
     ("int4", "gate_up", 64, "tiled"): (49033.0, 4352.0),
     ("int4", "gate_up", 1, "tiled"): (46148.8, 68.0),
     ("int4", "gate_up", 2048, "tiled"): (604139.4, 312730.8),
+    ("fp8", "gate_up", 2048, "tiled"): (933505.9, 278087.5),
 }
 FETCH_CAL, WRITE_CAL = 2.0, 1.0
 
@@ -570,8 +571,10 @@ def profile(torch, gen, dev, spec, launches):
     m = int(m)
     # kind "int4silu": gate_up with the fused SiLU-and-mul store, on weights
     # interleaved at load time (awq_gate_up_silu_mul)
+    # ("int4silut": on the tiled copy of the interleaved weight)
     # kind "int4t" / "fp8t": the load-time tiled copy (tiled decode kernel)
-    fused = kind == "int4silu"
+    fused = kind in ("int4silu", "int4silut")
+    fused_tiled = kind == "int4silut"
     if fused:
         kind = "int4"
     tiled_w = kind in ("int4t", "fp8t")
@@ -587,6 +590,8 @@ def profile(torch, gen, dev, spec, launches):
         from hydraserve_amd.kernels import awq_gate_up_silu_mul, interleave_gate_up
 
         ws = [interleave_gate_up(w) for w in ws]
+        if fused_tiled:
+            ws = tiled("int4", ws)
     c = Case(kind, name, n, k, m, ws, x)
     for i in range(launches):
         if fused:
