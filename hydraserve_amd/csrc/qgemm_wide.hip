@@ -391,25 +391,50 @@ struct Wide {
     }
     const int pf = unit_owner(ts, a.U, a.P), pl = unit_owner(te - 1, a.U, a.P);
     const auto pr = partial_rsrc(a.partials);
-    const uint32_t mine = slot_off(v, partial_slot(v, t, a.G, a.U, a.P));
+    // A range that comes from earlier tiles and ends in this one reaches it
+    // last (the other contributors work on it at the start of their ranges,
+    // or have only this tile), so it first looks at the
+    // arrival counter: when every other contributor has arrived, it settles
+    // with its own sums from the accumulators and stores no partial.
+    // Otherwise (or when it does not end here) it stores its partial and
+    // arrives; whoever arrives last settles from the stored partials.  No
+    // workgroup waits for another, and the sum runs in workgroup order
+    // either way, so the result does not depend on who settles.
+    bool own = false;
+    if (u0 < ts && u1 <= te) {
+      if (tid == 0)
+        sm.flag = __hip_atomic_load(&a.counters[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == pl - pf;
+      __syncthreads();
+      own = sm.flag != 0;
+    }
+    if (!own) {
+      const uint32_t mine = slot_off(v, partial_slot(v, t, a.G, a.U, a.P));
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+      for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < 2; ++j) {
 #pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4)
-          store_partial4(pr, mine + part_off((wave * MI + i) * 2 + j, c4, lane),
-                         f32x4_t{acc[i][j][4 * c4], acc[i][j][4 * c4 + 1], acc[i][j][4 * c4 + 2], acc[i][j][4 * c4 + 3]});
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    if (!arrive_last(a.counters, t, pl - pf + 1, &sm.flag)) return;
-    // Sum every contributor's slot (ours included) in workgroup order, two
-    // row blocks at a time: all 16 of a contributor's 16-byte loads for them
-    // are in flight before any is summed.
+          for (int c4 = 0; c4 < 4; ++c4)
+            store_partial4(pr, mine + part_off((wave * MI + i) * 2 + j, c4, lane),
+                           f32x4_t{acc[i][j][4 * c4], acc[i][j][4 * c4 + 1], acc[i][j][4 * c4 + 2], acc[i][j][4 * c4 + 3]});
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      if (!arrive_last(a.counters, t, pl - pf + 1, &sm.flag)) return;
+    }
+    // Sum every contributor's partial in workgroup order, two row blocks at
+    // a time: all 16 of a contributor's 16-byte loads for them are in flight
+    // before any is summed.
 #pragma unroll
     for (int i0 = 0; i0 < MI; i0 += 2) {
       f32x16_t sum[2][2] = {};
       for (int q = pf; q <= pl; ++q) {
+        if (own && q == v) {
+#pragma unroll
+          for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) sum[ii][j] += acc[i0 + ii][j];
+          continue;
+        }
         const uint32_t base = slot_off(q, partial_slot(q, t, a.G, a.U, a.P));
         f32x4_t x[2][2][4];
 #pragma unroll
